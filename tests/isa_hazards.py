@@ -75,3 +75,60 @@ def in_flight_uses(lines: list[str]) -> list[str]:
         if any(touched & p for p in pending):
             found.append(text)
     return found
+
+
+# ---------------------------------------------------------------------------
+# VALU write of an SGPR followed too closely by a vector-memory instruction
+# that reads it.  gfx9-family parts (gfx950 included) need 5 wait states
+# between a VALU instruction that writes an SGPR (v_readlane,
+# v_readfirstlane, a VOP3 compare or carry-out) and a VMEM instruction that
+# reads that SGPR as its resource descriptor, soffset or saddr; otherwise the
+# memory instruction can use the old value.  The compiler pads its own
+# instructions, but not a VMEM instruction written as inline assembly: there
+# a stale descriptor base sends the access to an unrelated address.
+
+_VMEM_ANY = ("buffer_", "global_", "flat_", "scratch_")
+_VALU_SGPR_CARRY = ("v_add_co", "v_sub_co", "v_subrev_co", "v_addc_co", "v_subb_co", "v_subbrev_co",
+                    "v_div_scale", "v_mad_u64", "v_mad_i64")
+VMEM_SGPR_WAIT_STATES = 5
+
+
+def _sregs(token: str) -> set[int]:
+    m = re.match(r"s\[(\d+):(\d+)\]", token)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"s(\d+)$", token)
+    return {int(m.group(1))} if m else set()
+
+
+def vmem_sgpr_hazards(lines: list[str]) -> list[tuple[str, int]]:
+    """(VMEM instruction, wait states since the VALU write) for every VMEM
+    instruction that reads an SGPR written by a VALU instruction fewer than
+    5 wait states earlier.  Linear walk in layout order; a label resets
+    nothing (conservative across fall-through), s_nop N counts N + 1."""
+    recent: list[tuple[set[int], int]] = []
+    found = []
+    for raw in lines:
+        text = raw.split(";")[0].strip()
+        if not text or text.startswith(".") or text.endswith(":"):
+            continue
+        op = text.split()[0]
+        args = [a.strip() for a in text[len(op):].split(",")]
+        if op.startswith(_VMEM_ANY):
+            reads = set()
+            for a in args:
+                if a:
+                    reads |= _sregs(a.split()[0])
+            for written, states in recent:
+                if written & reads and states < VMEM_SGPR_WAIT_STATES:
+                    found.append((text, states))
+        m = re.match(r"s_nop\s+(\d+)", text)
+        step = int(m.group(1)) + 1 if m else 1
+        recent = [(w, s + step) for w, s in recent if s + step < VMEM_SGPR_WAIT_STATES]
+        if op.startswith("v_") and args and args[0]:
+            dst = _sregs(args[0].split()[0])
+            if len(args) > 1 and op.startswith(_VALU_SGPR_CARRY):
+                dst |= _sregs(args[1].split()[0])
+            if dst:
+                recent.append((dst, 0))
+    return found
