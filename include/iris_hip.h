@@ -34,6 +34,10 @@ extern "C" {
 #define IRIS_ERR_LAUNCH 2           /* the HIP runtime rejected a kernel launch */
 #define IRIS_ERR_WORKSPACE 3        /* split-KV workspace missing or too small */
 
+/* Bytes of split-KV arrival counters at the head of a decode workspace for a
+ * batch of `batch` sequences: 128 uint32 per sequence, rounded up to 256. */
+#define IRIS_COUNTER_BYTES(batch) ((((int64_t)(batch) * 512) + 255) / 256 * 256)
+
 /*
  * Fused RoPE(K) + group-32 INT4 quantisation of K and V + nibble packing +
  * paged scatter.  Replaces the TileLang launch of `_rope_int4_paged_append`
@@ -134,21 +138,27 @@ int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, i
  *                output_is_f32 != 0 (fp32 is a test aid: the values before
  *                the final rounding)
  *   workspace    device buffer of at least the planned workspace bytes when
- *                max_chunks > 1 (may be NULL otherwise).  It must be
- *                zero-filled before its first use: its head holds one
- *                arrival counter per (sequence, kv block), and the chunks
- *                of a split sequence are merged inside this launch by the
- *                workgroup that arrives last, which resets the counter to
- *                zero.  Where the counters and the partial results sit
- *                depends on the plan and the shapes, so a workspace must be
- *                zero-filled again before a call whose plan or shapes differ
- *                from the previous call's (or that goes to the FP16 kernel).
- *                Calls that share a workspace must not overlap in time
- *                (issue them on one stream).
+ *                max_chunks > 1 (may be NULL otherwise).  Its first
+ *                IRIS_COUNTER_BYTES(batch) bytes are the split-KV arrival
+ *                counters, 128 uint32 per sequence at the same place for
+ *                every kernel, plan and shape (the FP16 decode included);
+ *                the chunks of a split sequence are merged inside this
+ *                launch by the workgroup that arrives last, which resets its
+ *                counter, so every call leaves them at zero.  The bytes
+ *                after them hold partial results that each call rewrites.
+ *                Zero-fill the counter region before the first call, and
+ *                again before a call whose batch exceeds the previous
+ *                call's (the previous call's partials may cover the
+ *                counters of the extra sequences).  Calls that share a
+ *                workspace must not overlap in time (issue them on one
+ *                stream).
  *   chunk_tiles, max_chunks, waves_per_block: from iris_decode_plan, as
  *                it returned them (|chunk_tiles| at most 64; a negative
  *                chunk_tiles selects the page kernel's balanced split, for
- *                ragged lengths the plan knew)
+ *                ragged lengths the plan knew: it stays valid while the
+ *                lengths' 32-token tiles, summed, are at most 64 *
+ *                max_chunks; past that the launch writes NaN into every
+ *                output element rather than a wrong result)
  *
  * page_size must be 16, head_dim 64 or 128, num_q_heads / num_kv_heads at
  * most 16 (fused_attention.py:390-403).  Page ids and lengths are not
@@ -193,11 +203,11 @@ int iris_fp16_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_hea
  *   block_table, seq_lens, output, output_is_f32: as for
  *                iris_int4_paged_decode_attention
  *   workspace    at least the planned workspace bytes when max_chunks > 1,
- *                zero-filled before its first use (one arrival counter per
- *                (sequence, kv head) at its head; every call leaves them at
- *                zero) and again before a call whose plan or shapes differ
- *                from the previous call's (or that went to an INT4 kernel).
- *                Calls sharing a workspace must not overlap in time.
+ *                with the counter region of iris_int4_paged_decode_attention
+ *                (the same layout, shared with the INT4 kernels): zero-filled
+ *                before the first call and before a call whose batch exceeds
+ *                the previous call's.  Calls sharing a workspace must not
+ *                overlap in time.
  *   chunk_pages, max_chunks: from iris_fp16_decode_plan
  *
  * page_size must be 16, head_dim 64 or 128, num_q_heads / num_kv_heads at

@@ -92,22 +92,21 @@ __global__ __launch_bounds__(256) void rope_int4_paged_append_kernel(
             half2_t b = oth * as_half2(sx[k][q]);  // x'*sin, rounded to fp16
             kr[q] = lo_half ? a - b : a + b;       // rounded to fp16
             vr[q] = as_half2(vx[k][q]);
-            kmax2 = __builtin_elementwise_max(kmax2, __builtin_elementwise_abs(kr[q]));
-            vmax2 = __builtin_elementwise_max(vmax2, __builtin_elementwise_abs(vr[q]));
+            kmax2 = amax_max(kmax2, __builtin_elementwise_abs(kr[q]));
+            vmax2 = amax_max(vmax2, __builtin_elementwise_abs(vr[q]));
         }
-        float kmax = fmaxf((float)kmax2.x, (float)kmax2.y);
-        float vmax = fmaxf((float)vmax2.x, (float)vmax2.y);
+        float kmax = amax_max((float)kmax2.x, (float)kmax2.y);
+        float vmax = amax_max((float)vmax2.x, (float)vmax2.y);
         // Quad = one 32-dim group.
-        kmax = fmaxf(kmax, __shfl_xor(kmax, 1, 64));
-        vmax = fmaxf(vmax, __shfl_xor(vmax, 1, 64));
-        kmax = fmaxf(kmax, __shfl_xor(kmax, 2, 64));
-        vmax = fmaxf(vmax, __shfl_xor(vmax, 2, 64));
+        kmax = amax_max(kmax, __shfl_xor(kmax, 1, 64));
+        vmax = amax_max(vmax, __shfl_xor(vmax, 1, 64));
+        kmax = amax_max(kmax, __shfl_xor(kmax, 2, 64));
+        vmax = amax_max(vmax, __shfl_xor(vmax, 2, 64));
 
         const half_t ks16 = scale_from_amax(kmax);
         const half_t vs16 = scale_from_amax(vmax);
-        const float ks = (float)ks16, vs = (float)vs16;
-        const uint32_t kword = quant_pack8(kr, ks, __builtin_amdgcn_rcpf(ks));
-        const uint32_t vword = quant_pack8(vr, vs, __builtin_amdgcn_rcpf(vs));
+        const uint32_t kword = pack_group8(kr, (float)ks16);
+        const uint32_t vword = pack_group8(vr, (float)vs16);
 
         if (live[k] && slot[k] >= 0) {
             const int64_t page = slot[k] / page_size;

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace iris {
 
 typedef _Float16 half_t;
@@ -24,5 +26,48 @@ enum Status : int {
 __device__ __forceinline__ half2_t as_half2(uint32_t x) { return __builtin_bit_cast(half2_t, x); }
 __device__ __forceinline__ uint32_t as_u32(half2_t x) { return __builtin_bit_cast(uint32_t, x); }
 __device__ __forceinline__ uint32_t as_u32(float x) { return __builtin_bit_cast(uint32_t, x); }
+
+// Split-KV arrival counters.  Every decode kernel keeps them in one region
+// at the head of its workspace, kCountersPerSeq uint32 per sequence
+// (sequence b's at [b * kCountersPerSeq, (b + 1) * kCountersPerSeq)), so
+// their place never depends on the kernel, its plan or the other shapes:
+// a workspace zero-filled once stays valid across calls of any layout, and
+// a call with a larger batch than before only needs the counters of the new
+// sequences zeroed.  Each launch leaves every counter it used at zero.
+constexpr int kCountersPerSeq = 128;
+inline int64_t counter_region_bytes(int64_t batch) { return (batch * kCountersPerSeq * 4 + 255) / 256 * 256; }
+
+// Arrival at a split-KV counter, by one thread after every partial of the
+// workgroup has been stored (and its stores have completed): acquire-release
+// at agent scope, so the partials published before each arrival are visible
+// to the workgroup whose arrival completes the count.  Returns true in that
+// workgroup, which also resets the counter for the next launch.
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expect) {
+    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old + 1 == expect;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return last;
+}
+
+// LDS a workgroup may use on gfx950 (per CU).
+constexpr int kMaxLdsBytes = 160 * 1024;
+
+// Lets KERNEL take up to kMaxLdsBytes of dynamic LDS on the current device
+// (HIP's default limit is 64 KiB).  Done once per device, remembered in an
+// atomic bitmask, so concurrent launches from several host threads are safe:
+// two threads racing here both set the same (idempotent) attribute.
+template <auto KERNEL>
+inline int allow_full_lds() {
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return kLaunchError;
+    const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+    if (bit != 0 && (done.load(std::memory_order_acquire) & bit)) return kOk;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(KERNEL), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            kMaxLdsBytes) != hipSuccess)
+        return kLaunchError;
+    done.fetch_or(bit, std::memory_order_release);
+    return kOk;
+}
 
 }  // namespace iris

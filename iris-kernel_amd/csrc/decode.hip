@@ -90,7 +90,7 @@ struct DecodeArgs {
     const int32_t* block_table;
     const int32_t* seq_lens;
     void* out;
-    uint32_t* counters;  // [B][n_kv_blocks] chunk arrivals; zero between calls
+    uint32_t* counters;  // counter kvb of sequence b at b * kCountersPerSeq + kvb; zero between calls
     float* ws_o;         // [B][max_chunks][n_kv_blocks][16 * D]  o / l, MFMA C order
     float* ws_ml;        // [B][max_chunks][n_kv_blocks][16][2]   (m, l), base-2 logits
     int out_f32;
@@ -775,15 +775,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void i
     }
     wait_vmem_all();
     __syncthreads();
-    uint32_t* const counter = a.counters + (int64_t)b * n_kvb + kvb;
+    uint32_t* const counter = a.counters + (int64_t)b * kCountersPerSeq + kvb;
     uint32_t* const ctl = reinterpret_cast<uint32_t*>(smem);  // wave 0's merge area is free now
-    if (threadIdx.x == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ctl[1] = (old + 1 == (uint32_t)n_chunks) ? 1u : 0u;
-    }
+    if (threadIdx.x == 0) ctl[1] = arrive_last(counter, (uint32_t)n_chunks) ? 1u : 0u;
     __syncthreads();
     if (ctl[1] == 0) return;
-    if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
     // Partials are read with plain buffer loads carrying the sc1 cache bit
     // (coherent across the XCDs' L2 caches, like the stores), which the
@@ -861,32 +857,27 @@ static int pick_kvw(int g, int hkv, int64_t batch, int64_t max_pages) {
 }
 
 // Dynamic LDS of one workgroup; above 64 KiB the kernel must be allowed to
-// use it (gfx950 has 160 KiB per CU).  Setting the attribute is idempotent.
+// use it (gfx950 has 160 KiB per CU): -1 if that fails.
 template <int D, int KVW>
 static int lds_bytes(int nw) {
     const int bytes = DecodeLayout<D, KVW>::WAVE_LDS * nw;
-    if (bytes > 65536) {
-        static bool raised = false;
-        if (!raised) {
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&int4_decode_kernel<D, KVW>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-            raised = true;
-        }
-    }
+    if (bytes > 65536 && allow_full_lds<&int4_decode_kernel<D, KVW>>() != kOk) return -1;
     return bytes;
 }
 
 template <int D, int KVW>
-static void launch_decode(dim3 grid, dim3 block, int nw, hipStream_t s, const DecodeArgs& a) {
+static int launch_decode(dim3 grid, dim3 block, int nw, hipStream_t s, const DecodeArgs& a) {
     const int lds = lds_bytes<D, KVW>(nw);
+    if (lds < 0) return kLaunchError;
     hipLaunchKernelGGL((int4_decode_kernel<D, KVW>), grid, block, lds, s, a);
+    return kOk;
 }
 
-// Workspace layout: [counters: B * n_kvb uint32, padded to 256 bytes]
+// Workspace layout: [counters: counter_region_bytes(B)]
 // [ws_o: B * max_chunks * n_kvb * 16 * D fp32][ws_ml: ... * 16 * 2 fp32].
-static int64_t counter_bytes(int64_t batch, int64_t n_kvb) { return (batch * n_kvb * 4 + 255) / 256 * 256; }
+// A split needs n_kvb <= kCountersPerSeq (every Hkv <= 128 qualifies).
 static int64_t workspace_bytes(int64_t batch, int64_t n_kvb, int64_t max_chunks, int64_t head_dim) {
-    return counter_bytes(batch, n_kvb) + batch * max_chunks * n_kvb * 16 * (head_dim + 2) * (int64_t)sizeof(float);
+    return counter_region_bytes(batch) + batch * max_chunks * n_kvb * 16 * (head_dim + 2) * (int64_t)sizeof(float);
 }
 
 }  // namespace iris
@@ -993,6 +984,7 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
         }
         max_chunks = (max_tiles + chunk_tiles - 1) / chunk_tiles;
     }
+    if (max_chunks > 1 && n_kvb > kCountersPerSeq) return kInvalidArgument;
     *out_chunk_tiles = (int32_t)chunk_tiles;
     *out_max_chunks = (int32_t)max_chunks;
     *out_waves = nw;
@@ -1046,26 +1038,28 @@ extern "C" int iris_int4_paged_decode_attention(
     a.ws_o = nullptr;
     a.ws_ml = nullptr;
     if (max_chunks > 1) {
+        if (a.n_kv_blocks > kCountersPerSeq) return kInvalidArgument;
         const int64_t need = workspace_bytes(batch, a.n_kv_blocks, max_chunks, head_dim);
         if (workspace == nullptr || workspace_bytes_avail < need) return kWorkspaceTooSmall;
         a.counters = (uint32_t*)workspace;
-        a.ws_o = (float*)((uint8_t*)workspace + counter_bytes(batch, a.n_kv_blocks));
+        a.ws_o = (float*)((uint8_t*)workspace + counter_region_bytes(batch));
         a.ws_ml = a.ws_o + batch * max_chunks * a.n_kv_blocks * 16 * head_dim;
     }
     const int64_t nblocks = batch * a.n_kv_blocks * (int64_t)max_chunks;
     if (nblocks > 0x7FFFFFFF) return kInvalidArgument;
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid((unsigned)nblocks), block(64 * waves_per_block);
+    int st;
     if (head_dim == 128) {
-        if (kvw == 4) launch_decode<128, 4>(grid, block, waves_per_block, s, a);
-        else if (kvw == 2) launch_decode<128, 2>(grid, block, waves_per_block, s, a);
-        else launch_decode<128, 1>(grid, block, waves_per_block, s, a);
+        if (kvw == 4) st = launch_decode<128, 4>(grid, block, waves_per_block, s, a);
+        else if (kvw == 2) st = launch_decode<128, 2>(grid, block, waves_per_block, s, a);
+        else st = launch_decode<128, 1>(grid, block, waves_per_block, s, a);
     } else {
-        if (kvw == 4) launch_decode<64, 4>(grid, block, waves_per_block, s, a);
-        else if (kvw == 2) launch_decode<64, 2>(grid, block, waves_per_block, s, a);
-        else launch_decode<64, 1>(grid, block, waves_per_block, s, a);
+        if (kvw == 4) st = launch_decode<64, 4>(grid, block, waves_per_block, s, a);
+        else if (kvw == 2) st = launch_decode<64, 2>(grid, block, waves_per_block, s, a);
+        else st = launch_decode<64, 1>(grid, block, waves_per_block, s, a);
     }
-    if (hipGetLastError() != hipSuccess) return kLaunchError;
+    if (st != kOk || hipGetLastError() != hipSuccess) return kLaunchError;
     return kOk;
 }
 

@@ -63,7 +63,7 @@ struct Args {
     const int32_t* block_table;
     const int32_t* seq_lens;
     void* out;
-    uint32_t* counters;  // [B][Hkv] arrivals; zero between calls
+    uint32_t* counters;  // counter j of sequence b at b * kCountersPerSeq + j; zero between calls
     float* ws_o;         // [B][Hkv][max_chunks][g][D] chunk o / l
     float* ws_ml;        // [B][Hkv][max_chunks][g][2] chunk (m, l), base-2 logits
     int out_f32;
@@ -318,13 +318,8 @@ void fp16_decode_kernel(Args a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     uint32_t* const ctl = reinterpret_cast<uint32_t*>(smem);
-    if (threadIdx.x == 0) {
-        uint32_t* const counter = a.counters + bj;
-        const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = old + 1 == (uint32_t)n_chunks;
-        if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ctl[0] = last ? 1u : 0u;
-    }
+    if (threadIdx.x == 0)
+        ctl[0] = arrive_last(a.counters + (int64_t)b * kCountersPerSeq + j, (uint32_t)n_chunks) ? 1u : 0u;
     __syncthreads();
     if (ctl[0] == 0) return;
     __syncthreads();  // ctl is overwritten by the merge weights below
@@ -397,12 +392,13 @@ void fp16_decode_kernel(Args a) {
 
 namespace {
 
-int64_t f16_counter_bytes(int64_t batch, int64_t hkv) { return (batch * hkv * 4 + 255) / 256 * 256; }
+// [counters: counter_region_bytes(B)][o: B * Hkv * max_chunks * g * D fp32][(m, l)]; a split
+// needs Hkv <= kCountersPerSeq.
 int64_t f16_workspace_bytes(int64_t batch, int64_t hq, int64_t hkv, int64_t head_dim, int64_t max_chunks) {
     const int64_t g = hq / hkv;
     const int64_t o = batch * hkv * max_chunks * g * head_dim * 4;
     const int64_t ml = batch * hkv * max_chunks * g * 2 * 4;
-    return f16_counter_bytes(batch, hkv) + (o + 255) / 256 * 256 + ml;
+    return counter_region_bytes(batch) + (o + 255) / 256 * 256 + ml;
 }
 
 }  // namespace
@@ -446,6 +442,7 @@ extern "C" int iris_fp16_decode_plan(int64_t batch, int64_t num_q_heads, int64_t
         max_chunks = (max_pages + chunk_pages - 1) / chunk_pages;
     }
     if (chunk_pages > f16::kMaxChunkPages) return kInvalidArgument;  // block_table too wide
+    if (max_chunks > 1 && num_kv_heads > kCountersPerSeq) return kInvalidArgument;
     *out_chunk_pages = (int32_t)chunk_pages;
     *out_max_chunks = (int32_t)max_chunks;
     *out_workspace_bytes =
@@ -486,14 +483,15 @@ extern "C" int iris_fp16_paged_decode_attention(const void* query, const void* k
     a.counters = nullptr;
     a.ws_o = a.ws_ml = nullptr;
     if (max_chunks > 1) {
+        if (num_kv_heads > kCountersPerSeq) return kInvalidArgument;
         const int64_t need = f16_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_chunks);
         if (workspace == nullptr || workspace_bytes_avail < need) return kWorkspaceTooSmall;
         const int64_t g = num_q_heads / num_kv_heads;
         uint8_t* const ws = (uint8_t*)workspace;
         a.counters = (uint32_t*)ws;
-        a.ws_o = (float*)(ws + f16_counter_bytes(batch, num_kv_heads));
+        a.ws_o = (float*)(ws + counter_region_bytes(batch));
         const int64_t o = batch * num_kv_heads * max_chunks * g * head_dim * 4;
-        a.ws_ml = (float*)(ws + f16_counter_bytes(batch, num_kv_heads) + (o + 255) / 256 * 256);
+        a.ws_ml = (float*)(ws + counter_region_bytes(batch) + (o + 255) / 256 * 256);
     }
     const int64_t nblocks = batch * num_kv_heads * (int64_t)max_chunks;
     if (nblocks > 0x7FFFFFFF) return kInvalidArgument;

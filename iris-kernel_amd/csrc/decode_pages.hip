@@ -80,6 +80,8 @@ constexpr int kLdsBudget = 160 * 1024;
 constexpr int kStages = 3;
 constexpr int kMergeGroup = 8;  // chunks merged by the last of each group
 constexpr int kMaxGroups = 64;  // groups merged by the last group
+constexpr int kSeqCounter = kCountersPerSeq - 1;  // a sequence's group-level arrival counter
+static_assert(kMaxGroups < kSeqCounter, "group counters and the sequence counter share a sequence's region");
 constexpr int kSC1 = 16;        // cache-policy bit sc1: device-coherent access
 constexpr int kNT = 2;          // cache-policy bit nt: streaming (the cache pages are read once)
 
@@ -98,7 +100,8 @@ struct Args {
     void* out;
     // Split-KV slots: chunk c of sequence b, done by logical workgroup
     // w = first(b) + c, owns slot w + b (unique; slots = workgroups + B).
-    uint32_t* counters;  // [slots] group arrivals (at the group's first chunk slot), then [B]; zero between calls
+    uint32_t* counters;  // sequence b: group gi's arrivals at b * kCountersPerSeq + gi, the groups' at
+                         // b * kCountersPerSeq + kSeqCounter; zero between calls
     float* p1_o;         // [slots][Hq][D]  chunk o / l
     float* p1_ml;        // [slots][Hq][2]  chunk (m, l), base-2 logits
     float* p2_o;         // [slots][Hq][D]  group o / l (group gi of b at slot first(b) + b + gi)
@@ -831,12 +834,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void int4_decode_pages_kernel(Args 
     // Arrival at a counter: true in the workgroup that completes `expect`
     // arrivals (which then resets the counter).
     auto arrive = [&](uint32_t* counter, int expect) -> bool {
-        if (threadIdx.x == 0) {
-            const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const bool last = old + 1 == (uint32_t)expect;
-            if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            ctl[0] = last ? 1u : 0u;
-        }
+        if (threadIdx.x == 0) ctl[0] = arrive_last(counter, (uint32_t)expect) ? 1u : 0u;
         __syncthreads();
         const bool last = ctl[0] != 0;
         __syncthreads();
@@ -846,7 +844,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void int4_decode_pages_kernel(Args 
     const int grp = chunk / kMergeGroup;
     const int n_groups = (n_chunks + kMergeGroup - 1) / kMergeGroup;
     const int members = min(kMergeGroup, n_chunks - grp * kMergeGroup);
-    if (!arrive(a.counters + (int64_t)first + b + grp * kMergeGroup, members)) return;
+    if (!arrive(a.counters + (int64_t)b * kCountersPerSeq + grp, members)) return;
     {
         const int64_t row = (int64_t)first + b + grp * kMergeGroup;
         const auto ro = page_rsrc(a.p1_o + row * total, part_o * members);
@@ -859,7 +857,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void int4_decode_pages_kernel(Args 
     }
     wait_vmcnt<0>();
     __syncthreads();
-    if (!arrive(a.counters + (int64_t)a.slots + b, n_groups)) return;
+    if (!arrive(a.counters + (int64_t)b * kCountersPerSeq + kSeqCounter, n_groups)) return;
     {
         const int64_t row2 = (int64_t)first + b;
         const auto ro = page_rsrc(a.p2_o + row2 * total, part_o * n_groups);
@@ -912,14 +910,20 @@ __global__ __launch_bounds__(64 * kMaxWaves) void int4_decode_pages_kernel(Args 
         // At most T ranges, so that none is empty and a sequence's chunks
         // are numbered without gaps (range workgroups past them have none).
         const long long Wl = (long long)W < T ? (long long)W : T;
+        if (T > (long long)kMaxChunkTiles * Wl) {
+            // The lengths outgrew the plan (a balanced plan made for fewer
+            // tokens): a range would not fit the page-id window.  Every
+            // workgroup sees the same T, so all of them take this branch and
+            // write NaN into the whole output instead of a wrong result.
+            const int64_t n_out = (int64_t)a.batch * a.n_q_heads * D;
+            for (int64_t i = (int64_t)blockIdx.x * BD + threadIdx.x; i < n_out; i += (int64_t)gridDim.x * BD) {
+                if (a.out_f32) reinterpret_cast<float*>(a.out)[i] = __builtin_nanf("");
+                else reinterpret_cast<half_t*>(a.out)[i] = __builtin_bit_cast(half_t, (uint16_t)0x7E00);
+            }
+            return;
+        }
         auto range_lo = [&](long long w) -> long long { return w * T / Wl; };
-        // (Plans keep every range within kMaxChunkTiles; a call whose lengths
-        // were not planned for is cut short there instead of overrunning the
-        // page-id window.)
-        auto range_hi = [&](long long w) -> long long {
-            const long long h = (w + 1) * T / Wl, l = w * T / Wl;
-            return h < l + kMaxChunkTiles ? h : l + kMaxChunkTiles;
-        };
+        auto range_hi = [&](long long w) -> long long { return (w + 1) * T / Wl; };
         long long carry = 0;
         for (int b0 = 0; b0 < a.batch; b0 += BD) {
             const int bb = b0 + (int)threadIdx.x;
@@ -1021,14 +1025,15 @@ struct WorkspaceLayout {
 
 int64_t round256(int64_t x) { return (x + 255) / 256 * 256; }
 
-// [counters: slots group arrivals, then batch sequence arrivals][chunk
-// partials: o, then (m, l)][group partials: o, then (m, l); only when a
-// sequence can have more than one group], each region 256-byte aligned.
+// [counters: counter_region_bytes(batch)][chunk partials: o, then (m, l)]
+// [group partials: o, then (m, l); only when a sequence can have more than
+// one group], each region 256-byte aligned.  Only the counters carry state
+// from one call to the next.
 WorkspaceLayout workspace_layout(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t slots, bool level2) {
     const int64_t s2 = level2 ? slots : 0;
     WorkspaceLayout w;
     w.counters = 0;
-    w.p1_o = round256((slots + batch) * 4);
+    w.p1_o = counter_region_bytes(batch);
     w.p1_ml = w.p1_o + round256(slots * num_q_heads * head_dim * 4);
     w.p2_o = w.p1_ml + round256(slots * num_q_heads * 2 * 4);
     w.p2_ml = w.p2_o + round256(s2 * num_q_heads * head_dim * 4);
@@ -1039,13 +1044,7 @@ WorkspaceLayout workspace_layout(int64_t batch, int64_t num_q_heads, int64_t hea
 template <int D, int GS, int HKV>
 int launch(dim3 grid, int lds, hipStream_t s, const pg::Args& a) {
     static_assert(pg::page_geom(HKV, D).nw == kWaves, "16 waves per workgroup");
-    static int raised = 0;  // largest dynamic LDS size enabled so far
-    if (lds > raised) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&pg::int4_decode_pages_kernel<D, GS, HKV>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
-            return kLaunchError;
-        raised = lds;
-    }
+    if (lds > 65536 && allow_full_lds<&pg::int4_decode_pages_kernel<D, GS, HKV>>() != kOk) return kLaunchError;
     hipLaunchKernelGGL((pg::int4_decode_pages_kernel<D, GS, HKV>), grid, dim3(64 * kWaves), lds, s, a);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchError;
 }

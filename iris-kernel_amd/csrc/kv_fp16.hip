@@ -125,14 +125,13 @@ __global__ __launch_bounds__(256) void quantize_pack_int4_kernel(const u32x4_t* 
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         v[q] = as_half2(vx[q]);
-        m2 = __builtin_elementwise_max(m2, __builtin_elementwise_abs(v[q]));
+        m2 = amax_max(m2, __builtin_elementwise_abs(v[q]));
     }
-    float amax = fmaxf((float)m2.x, (float)m2.y);
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));  // a quad is one 32-dim group
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    float amax = amax_max((float)m2.x, (float)m2.y);
+    amax = amax_max(amax, __shfl_xor(amax, 1, 64));  // a quad is one 32-dim group
+    amax = amax_max(amax, __shfl_xor(amax, 2, 64));
     const half_t s16 = scale_from_amax(amax);
-    const float s = (float)s16;
-    const uint32_t word = quant_pack8(v, s, __builtin_amdgcn_rcpf(s));
+    const uint32_t word = pack_group8(v, (float)s16);
     if (live) {
         packed[r * chunks + c] = word;
         if ((c & 3) == 0) scales[r * (head_dim >> 5) + (c >> 2)] = s16;

@@ -1,5 +1,5 @@
-// INT4 group quantiser arithmetic shared by the append kernel and the
-// device self-test.  Bit-exact with the reference quantiser
+// INT4 group quantiser arithmetic shared by the append and quantise-pack
+// kernels.  Bit-exact with the reference quantiser
 // (torch_eager_kv.py:75-86 in Hunter2030ZeRo/Iris-Kernel):
 //
 //   scale16 = RN16(max(amax / 7, 2^-14))
@@ -8,8 +8,15 @@
 // without an IEEE divide per value.  Both replacements below were checked
 // exhaustively against the reference formulas for every fp16 input that can
 // reach them (oracle/iris_oracle.c: ior_check_scale_mul,
-// ior_check_quant_fast), and the GPU instructions themselves are re-checked
-// by the device self-test.
+// ior_check_quant_fast); the GPU parity tests run them on every config.
+//
+// Non-finite groups follow torch: the group amax (torch.amax) and the clamp
+// (clamp_min) propagate NaN, so a group holding a NaN gets a NaN scale, and
+// a group holding an infinity (and no NaN) an infinite one.  torch's
+// fp32 -> fp16 conversion stores every NaN as 0x7E00.  With such a scale
+// every x / scale is +-0 or NaN, and float -> int8 turns both into 0, so all
+// codes of the group are 0 (the kernels use amax_max below for the group
+// maximum and pack_group8 for the codes).
 //
 // This file must be compiled with -ffp-contract=off: every multiply and add
 // below is a separately rounded fp32 operation.
@@ -25,8 +32,14 @@ constexpr float kOneSeventh = (float)(1.0 / 7.0);
 constexpr float kMinScale = 6.103515625e-05f;  // finfo(float16).tiny = 2^-14
 constexpr float kRoundMagic = 12582912.0f;     // 1.5 * 2^23
 
+// max as torch.amax computes it: a NaN operand gives NaN (v_maximum3_f32,
+// not the NaN-dropping v_max_f32).
+__device__ __forceinline__ float amax_max(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ half2_t amax_max(half2_t a, half2_t b) { return __builtin_elementwise_maximum(a, b); }
+
 __device__ __forceinline__ half_t scale_from_amax(float amax) {
-    float s = fmaxf(amax * kOneSeventh, kMinScale);
+    const float s = __builtin_elementwise_maximum(amax * kOneSeventh, kMinScale);  // clamp_min keeps NaN
+    if (s != s) return __builtin_bit_cast(half_t, (uint16_t)0x7E00);
     return (half_t)s;  // v_cvt_f16_f32, round to nearest even
 }
 
@@ -57,6 +70,13 @@ __device__ __forceinline__ uint32_t quant_pack8(const half2_t v[4], float s, flo
         word |= (lo | (hi << 4)) << (8 * q);
     }
     return word;
+}
+
+// quant_pack8 for a group whose stored scale is s: all-zero codes when s is
+// NaN or infinite (see the header comment).
+__device__ __forceinline__ uint32_t pack_group8(const half2_t v[4], float s) {
+    const uint32_t word = quant_pack8(v, s, __builtin_amdgcn_rcpf(s));
+    return __builtin_isfinite(s) ? word : 0u;
 }
 
 }  // namespace iris

@@ -10,10 +10,9 @@ same launch) through the C ABI ``iris_int4_paged_decode_attention``.
 
 Additions, all keyword-only and defaulted so existing calls are unchanged:
 ``tokens_per_split`` / ``waves_per_block`` override the split heuristic,
-``workspace`` supplies the split-KV buffer (zero-filled before its first
-use; every call leaves its arrival counters at zero again, and the wrapper
-clears it again before a call whose layout -- kernel and shapes -- differs
-from the previous call's).  Without one, a
+``workspace`` supplies the split-KV buffer (its head holds 128 arrival
+counters per sequence, which every call leaves at zero; the wrapper zeroes
+that region whenever a call's batch exceeds the previous call's).  Without one, a
 zero-filled workspace is cached per (device, stream), so calls on one stream
 share it safely and calls on different streams never do.  An fp32 ``output``
 tensor receives the values before the final fp16 rounding (test aid).
@@ -49,6 +48,15 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
     return ct.value, mc.value, nw.value, ws.value
 
 
+def _qk_scale(head_dim: int, softmax_scale) -> float:
+    """The logit scale: the reference wrapper passes 0.0 for None
+    (fused_attention.py:523) and its kernel maps 0.0 to head_dim ** -0.5
+    (fused_attention.py:50), so None and an explicit 0.0 both mean that."""
+    if softmax_scale is None or float(softmax_scale) == 0.0:
+        return head_dim ** -0.5
+    return float(softmax_scale)
+
+
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 
 
@@ -81,19 +89,29 @@ def _check_state(device: torch.device, stream: int) -> tuple[torch.Tensor, torch
     return bufs
 
 
-_LAYOUTS: dict[tuple[int, int], tuple] = {}
+_COUNTERS_PER_SEQ = 128  # kCountersPerSeq of csrc/common.h
 
 
-def _ready_workspace(device: torch.device, ws_bytes: int, layout: tuple,
+def counter_region_bytes(batch: int) -> int:
+    """Bytes at the head of a split-KV workspace that hold the arrival
+    counters of `batch` sequences (the same for every decode kernel)."""
+    return (batch * _COUNTERS_PER_SEQ * 4 + 255) // 256 * 256
+
+
+# workspace (pointer, bytes) -> the batch whose counter region is known to be zero
+_ZEROED: dict[tuple[int, int], int] = {}
+
+
+def _ready_workspace(device: torch.device, ws_bytes: int, batch: int,
                      workspace: torch.Tensor | None) -> torch.Tensor:
     """The split-KV workspace for a call, its arrival counters at zero.
 
-    Each kernel leaves its own counters at zero, but where the counters and
-    the partial results sit depends on the layout (kernel and shapes): after
-    a call with another layout, bytes that now hold counters may hold
-    partials.  So a workspace is cleared (a fill kernel on the current
-    stream) whenever the layout of the call differs from the one it last
-    served; calls that repeat a layout pay nothing."""
+    Every kernel keeps its counters at the head of the workspace, 128 per
+    sequence, and leaves them at zero; the bytes after them hold partial
+    results that each call rewrites.  A call with batch B therefore finds
+    the counters of sequences below the last call's batch at zero; only when
+    B exceeds that batch does the counter region need a fill (one small fill
+    kernel on the current stream)."""
     if workspace is None:
         workspace = _stream_workspace(device, ws_bytes)
     elif workspace.numel() * workspace.element_size() < ws_bytes:
@@ -101,9 +119,9 @@ def _ready_workspace(device: torch.device, ws_bytes: int, layout: tuple,
     elif not workspace.is_contiguous():
         raise ValueError("workspace must be contiguous")
     key = (workspace.data_ptr(), workspace.numel() * workspace.element_size())
-    if _LAYOUTS.get(key) != layout:
-        workspace.reshape(-1).view(torch.uint8)[:ws_bytes].zero_()
-        _LAYOUTS[key] = layout
+    if _ZEROED.get(key, 0) < batch:
+        workspace.reshape(-1).view(torch.uint8)[:counter_region_bytes(batch)].zero_()
+    _ZEROED[key] = batch  # the partials of this call may overwrite counters of later sequences
     return workspace
 
 
@@ -113,10 +131,7 @@ def _launch_decode(query, k_data, v_data, k_scale, v_scale, block_table, seq_len
     batch, num_q_heads, head_dim = query.shape
     num_pages, page_size, num_kv_heads, _ = k_data.shape
     if ws_bytes > 0:
-        # (the general kernel's kv heads per wave also follow the block_table width)
-        workspace = _ready_workspace(query.device, ws_bytes,
-                                     ("int4", tuple(plan), batch, num_q_heads, num_kv_heads, head_dim,
-                                      block_table.shape[1]), workspace)
+        workspace = _ready_workspace(query.device, ws_bytes, batch, workspace)
         ws_ptr, ws_len = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     else:
         ws_ptr, ws_len = 0, 0
@@ -191,7 +206,17 @@ def _validate_common_decode_inputs(query, block_table, seq_lens, *, num_pages: i
     capability = torch.cuda.get_device_capability(device)
     if capability < (7, 0):
         raise RuntimeError(f"unsupported CUDA compute capability: {capability}")
-    return batch, num_query_heads, head_dim, total, longest
+    return batch, num_query_heads, head_dim, total, longest, bt, sl
+
+
+def _dense(t: torch.Tensor, align: int) -> torch.Tensor:
+    """t itself when contiguous and `align`-byte aligned, else a dense copy
+    (a block_table[:, :n] slice or a q split out of a fused qkv projection)."""
+    if t.is_contiguous() and t.data_ptr() % align == 0:
+        return t
+    out = torch.empty(t.shape, dtype=t.dtype, device=t.device)  # fresh allocations are 256-byte aligned
+    out.copy_(t)
+    return out
 
 
 def fused_int4_paged_decode_attention(
@@ -225,7 +250,7 @@ def fused_int4_paged_decode_attention(
     _, _, head_dim = query.shape
     if cache_page_size != page_size or packed_dim * 2 != head_dim:
         raise ValueError("packed cache shape does not match query/page_size")
-    batch, num_q_heads, head_dim, total, longest = _validate_common_decode_inputs(
+    batch, num_q_heads, head_dim, total, longest, block_table, seq_lens = _validate_common_decode_inputs(
         query, block_table, seq_lens, num_pages=num_pages, num_kv_heads=num_kv_heads,
         page_size=page_size)
     scale_shape = (num_pages, page_size, num_kv_heads, head_dim // group_size)
@@ -250,11 +275,11 @@ def fused_int4_paged_decode_attention(
         raise ValueError("output must be on the same device as query")
     if batch == 0:
         return output
-    scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
+    scale = _qk_scale(head_dim, softmax_scale)
     plan = decode_plan(batch, num_q_heads, num_kv_heads, head_dim, block_table.shape[1],
                        total, longest, tokens_per_split, waves_per_block)
-    _launch_decode(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, scale,
-                   plan, workspace)
+    _launch_decode(_dense(query, 16), k_data, v_data, k_scale, v_scale, block_table, seq_lens, output,
+                   scale, plan, workspace)
     return output
 
 
@@ -271,7 +296,7 @@ def _int4_paged_decode_attention(query, k_data, v_data, k_scale, v_scale, block_
     batch, num_q_heads, _ = query.shape
     if batch == 0:
         return
-    scale = head_dim ** -0.5 if softmax_scale == 0.0 else float(softmax_scale)
+    scale = _qk_scale(head_dim, softmax_scale)
     plan = decode_plan(batch, num_q_heads, k_data.shape[2], head_dim, block_table.shape[1])
     _launch_decode(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, scale,
                    plan)
@@ -299,8 +324,7 @@ def _launch_fp16_decode(query, k_cache, v_cache, block_table, seq_lens, output, 
     batch, num_q_heads, head_dim = query.shape
     num_pages, page_size, num_kv_heads, _ = k_cache.shape
     if ws_bytes > 0:
-        workspace = _ready_workspace(query.device, ws_bytes,
-                                     ("fp16", tuple(plan), batch, num_q_heads, num_kv_heads, head_dim), workspace)
+        workspace = _ready_workspace(query.device, ws_bytes, batch, workspace)
         ws_ptr, ws_len = workspace.data_ptr(), workspace.numel() * workspace.element_size()
     else:
         ws_ptr, ws_len = 0, 0
@@ -343,7 +367,7 @@ def fused_fp16_paged_decode_attention(
     _, _, head_dim = query.shape
     if cache_page_size != page_size or cache_dim != head_dim:
         raise ValueError("FP16 cache shape does not match query/page_size")
-    batch, num_q_heads, head_dim, total, longest = _validate_common_decode_inputs(
+    batch, num_q_heads, head_dim, total, longest, block_table, seq_lens = _validate_common_decode_inputs(
         query, block_table, seq_lens, num_pages=num_pages, num_kv_heads=num_kv_heads,
         page_size=page_size)
     if k_cache.dtype != torch.float16 or v_cache.dtype != torch.float16:
@@ -358,10 +382,11 @@ def fused_fp16_paged_decode_attention(
         raise ValueError("output must be on the same device as query")
     if batch == 0:
         return output
-    scale = head_dim ** -0.5 if softmax_scale is None else float(softmax_scale)
+    scale = _qk_scale(head_dim, softmax_scale)
     plan = fp16_decode_plan(batch, num_q_heads, num_kv_heads, head_dim, block_table.shape[1], total,
                             longest, tokens_per_split)
-    _launch_fp16_decode(query, k_cache, v_cache, block_table, seq_lens, output, scale, plan, workspace)
+    _launch_fp16_decode(_dense(query, 16), k_cache, v_cache, block_table, seq_lens, output, scale, plan,
+                        workspace)
     return output
 
 
@@ -379,5 +404,5 @@ def _fp16_paged_decode_attention(query, k_cache, v_cache, block_table, seq_lens,
         return
     num_kv_heads = k_cache.shape[2]
     plan = fp16_decode_plan(batch, num_q_heads, num_kv_heads, head_dim, block_table.shape[1])
-    scale = head_dim ** -0.5 if softmax_scale == 0.0 else float(softmax_scale)
+    scale = _qk_scale(head_dim, softmax_scale)
     _launch_fp16_decode(query, k_cache, v_cache, block_table, seq_lens, output, scale, plan)

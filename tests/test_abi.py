@@ -124,23 +124,28 @@ def general_kvw(B, Hq, Hkv, max_pages):
     return kvw
 
 
+def counter_bytes(B):
+    """The arrival-counter region every decode kernel keeps at the head of its
+    workspace: 128 uint32 per sequence (IRIS_COUNTER_BYTES)."""
+    return (B * 128 * 4 + 255) // 256 * 256
+
+
 def general_workspace(B, Hq, Hkv, D, max_chunks, max_pages):
     """Workspace bytes of the general kernel's split (decode.hip)."""
     n_kvb = Hkv // general_kvw(B, Hq, Hkv, max_pages)
-    counters = (B * n_kvb * 4 + 255) // 256 * 256
-    return counters + B * max_chunks * n_kvb * 16 * (D + 2) * 4
+    return counter_bytes(B) + B * max_chunks * n_kvb * 16 * (D + 2) * 4
 
 
 def pages_workspace(B, Hq, D, max_chunks, balanced=False):
     """Workspace bytes of the page kernel's split (decode_pages.hip): one slot
     per (workgroup, sequence) pair a workgroup can work on (workgroups + B:
     B x max_chunks workgroups in chunk mode, max_chunks in the balanced
-    mode); group and sequence counters, chunk partials, and group partials
-    when a sequence can span more than one group of 8 chunks."""
+    mode); the counter region, chunk partials, and group partials when a
+    sequence can span more than one group of 8 chunks."""
     r = lambda x: (x + 255) // 256 * 256  # noqa: E731
     slots = (max_chunks if balanced else B * max_chunks) + B
     s2 = slots if max_chunks > 8 else 0
-    return (r((slots + B) * 4) + r(slots * Hq * D * 4) + r(slots * Hq * 2 * 4)
+    return (counter_bytes(B) + r(slots * Hq * D * 4) + r(slots * Hq * 2 * 4)
             + r(s2 * Hq * D * 4) + r(s2 * Hq * 2 * 4))
 
 

@@ -107,6 +107,44 @@ def test_ties_subnormals_and_extremes(device):
     assert_same(ref, gpu)
 
 
+def test_nan_and_inf_rows(device):
+    # torch.amax and clamp_min propagate NaN: a group holding a NaN gets the
+    # scale 0x7E00 (torch's fp16 NaN), one holding an infinity 0x7C00, and
+    # every code of such a group is 0 (x / scale is +-0 or NaN, and float ->
+    # int8 gives 0).  RoPE turns an infinite K next to a zero sine into NaN
+    # (inf * 0), so K rows at position 0 exercise that path too.
+    log("append: NaN / inf rows")
+    g = torch.Generator().manual_seed(23)
+    T, H, D = 48, 4, 128
+    key = torch.randn(T, H, D, generator=g).to(torch.float16)
+    value = torch.randn(T, H, D, generator=g).to(torch.float16)
+    nan, inf = float("nan"), float("inf")
+    key[0, 0, 3] = nan
+    key[1, 1, 70] = inf
+    key[2, 2, 100] = -inf
+    key[3, 3, 5] = inf
+    key[3, 3, 37] = nan
+    value[4, 0, 31] = nan
+    value[5, 1, 64] = -inf
+    value[6, 2, :] = inf
+    value[7, 3, 96:] = nan
+    key[8:16] = nan
+    value[16:24, :, 32:64] = -inf
+    pos = torch.randint(0, 40, (T,), generator=g, dtype=torch.int32)
+    pos[1:4] = 0  # sin = 0: inf * 0 = NaN in the rotated partner dims
+    slots = torch.randperm(4 * 16, generator=g)[:T].to(torch.int32)
+    cos, sin = workloads.make_rope_cache(40, D)
+    cache = (torch.randint(0, 256, (4, 16, H, D // 2), dtype=torch.uint8, generator=g),
+             torch.randint(0, 256, (4, 16, H, D // 2), dtype=torch.uint8, generator=g),
+             torch.randn(4, 16, H, D // 32, generator=g).to(torch.float16),
+             torch.randn(4, 16, H, D // 32, generator=g).to(torch.float16))
+    ref, gpu = run_both(device, key, value, pos, slots, cos, sin, cache, D)
+    # the case really has non-finite groups on both sides
+    ks = ref[2].view(torch.int16)
+    assert (ks == 0x7E00).any() and (ref[3].view(torch.int16) == 0x7C00).any()
+    assert_same(ref, gpu)
+
+
 def test_private_positional_handle(device):
     case = workloads.append_case(2)
     cache = case.empty_cache(fill="random")

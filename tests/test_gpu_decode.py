@@ -189,6 +189,55 @@ def test_balanced_split_ragged_batches(device, case):
         assert_attention_close(out, want, f"{case} call {i}")
 
 
+def test_stale_balanced_plan_writes_nan(device):
+    # A balanced plan made for short ragged lengths, launched (through the
+    # C ABI's launch path) with lengths whose tiles exceed what its ranges
+    # can cover: every output element is NaN, not a silently truncated
+    # result, and the workspace stays usable for the next correct call.
+    from iris_kernel import fused_attention as fa
+
+    case, cpu, gpu = prepared(2, device)
+    q, bt, full = to(device, case.query, case.block_table, case.seq_lens)
+    B, hq, d = q.shape
+    short = torch.full((B,), 40, dtype=torch.int32)
+    short[::2] = 700
+    plan = decode_plan(B, hq, 8, d, bt.shape[1], int(short.sum()), int(short.max()), 0, 16)
+    assert plan[0] < 0 and plan[2] == 16, plan
+    assert 32 * (4096 // 32) > 64 * plan[1], plan  # the full lengths outgrow it
+    ws = torch.zeros(max(plan[3], 1), dtype=torch.uint8, device=device)
+    out = torch.empty(B, hq, d, dtype=torch.float32, device=device)
+    fa._launch_decode(q, *gpu, bt, short.to(device), out, d ** -0.5, plan, ws)
+    torch.cuda.synchronize(device)
+    assert_attention_close(out, eager_fp32(case, cpu, seq_lens=short), "planned lengths")
+    for dtype in (torch.float32, torch.float16):
+        bad = torch.zeros(B, hq, d, dtype=dtype, device=device)
+        fa._launch_decode(q, *gpu, bt, full, bad, d ** -0.5, plan, ws)
+        torch.cuda.synchronize(device)
+        assert torch.isnan(bad.float()).all(), f"{dtype}: a stale plan must poison every output"
+    fa._launch_decode(q, *gpu, bt, short.to(device), out, d ** -0.5, plan, ws)
+    torch.cuda.synchronize(device)
+    assert_attention_close(out, eager_fp32(case, cpu, seq_lens=short), "after the stale call")
+
+
+def test_workspace_across_batches_and_kernels(device):
+    # One workspace for calls whose batch grows and shrinks and whose kernel
+    # changes (page kernel, general kernel): the counters sit at a fixed
+    # place per sequence, and the wrapper zeroes the counter region only when
+    # the batch grows past the previous call's.
+    case, cpu, gpu = prepared(2, device)
+    if 2 not in _WANT:
+        _WANT[2] = eager_fp32(case, cpu)
+    want = _WANT[2]
+    q, bt, sl = to(device, case.query, case.block_table, case.seq_lens)
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device=device)
+    for n, waves in ((32, 16), (4, 16), (32, 4), (8, 4), (32, 16), (1, 16), (32, 4)):
+        out = torch.empty(n, q.shape[1], q.shape[2], dtype=torch.float32, device=device)
+        fused_int4_paged_decode_attention(q[:n], *gpu, bt[:n], sl[:n], out, waves_per_block=waves,
+                                          tokens_per_split=512, workspace=ws)
+        torch.cuda.synchronize(device)
+        assert_attention_close(out, want[:n], f"batch {n} waves {waves}")
+
+
 @pytest.mark.parametrize("waves", [1, 2, 3, 4, 16])
 def test_waves_per_block_invariance(device, waves):
     case, cpu, gpu = prepared(1, device)
@@ -254,6 +303,31 @@ def test_custom_softmax_scale_and_private_handle(device):
     _int4_paged_decode_attention(q, *gpu, bt, sl, out, 64, 16, 32, 16, 32, 128, 0.0)
     torch.cuda.synchronize(device)
     assert_attention_close(out, eager_fp32(case, cpu), "private handle")
+
+
+def test_zero_softmax_scale_and_strided_inputs(device):
+    # The reference wrapper hands softmax_scale=0.0 to its kernel, which
+    # reads 0.0 as head_dim ** -0.5 (fused_attention.py:50, :523): an
+    # explicit 0.0 gives the default result.  Strided inputs (q split out of
+    # a fused qkv tensor, a block_table column slice, a strided seq_lens)
+    # give the same result as dense ones.
+    case, cpu, gpu = prepared(1, device)
+    want = eager_fp32(case, cpu)
+    got = run(case, gpu, device, torch.float32, softmax_scale=0.0)
+    assert_attention_close(got, want, "softmax_scale=0.0")
+    q, bt, sl = to(device, case.query, case.block_table, case.seq_lens)
+    B, hq, d = q.shape
+    qkv = torch.empty(B, 3 * hq, d, dtype=q.dtype, device=device)
+    qkv[:, :hq] = q
+    wide_bt = torch.full((B, bt.shape[1] + 5), -1, dtype=torch.int32, device=device)
+    wide_bt[:, :bt.shape[1]] = bt
+    sl2 = torch.stack([sl, torch.zeros_like(sl)], dim=1)[:, 0]
+    assert not qkv[:, :hq].is_contiguous() and not wide_bt[:, :bt.shape[1]].is_contiguous()
+    assert not sl2.is_contiguous()
+    out = torch.empty(B, hq, d, dtype=torch.float32, device=device)
+    fused_int4_paged_decode_attention(qkv[:, :hq], *gpu, wide_bt[:, :bt.shape[1]], sl2, out)
+    torch.cuda.synchronize(device)
+    assert_attention_close(out, want, "strided inputs")
 
 
 def test_validation_errors(device):

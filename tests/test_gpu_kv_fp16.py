@@ -186,6 +186,24 @@ def _edge_values(d: int) -> torch.Tensor:
     return torch.stack([t, -t, t * 0.001], dim=1)
 
 
+def _non_finite_rows(d):
+    # NaN / +-inf in single dims, whole groups and whole rows: the group's
+    # scale becomes 0x7E00 (NaN) or 0x7C00 (inf) and its codes 0, as
+    # torch.amax / clamp_min / float->int8 give them.
+    g = torch.Generator().manual_seed(d)
+    x = torch.randn(16, 3, d, generator=g).to(torch.float16)
+    nan, inf = float("nan"), float("inf")
+    x[0, 0, 1] = nan
+    x[1, 1, d - 1] = inf
+    x[2, 2, 33 % d] = -inf
+    x[3, 0, 0] = inf
+    x[3, 0, 1] = nan
+    x[4, :, :32] = nan
+    x[5, 1, :] = -inf
+    x[6] = nan
+    return x
+
+
 @pytest.mark.parametrize("head_dim", [64, 128, 256, 512])
 def test_quantize_pack_matches_eager(device, head_dim):
     # test_correctness.py:465-592 (head_dim 64, 128, 256; 7 x 4 random
@@ -193,7 +211,8 @@ def test_quantize_pack_matches_eager(device, head_dim):
     torch.manual_seed(3407)
     for name, x in (("random", torch.randn(7, 4, head_dim, dtype=torch.float16)),
                     ("edges", _edge_values(head_dim)),
-                    ("bulk", (torch.randn(4096, 8, head_dim) * 4).to(torch.float16))):
+                    ("bulk", (torch.randn(4096, 8, head_dim) * 4).to(torch.float16)),
+                    ("non-finite", _non_finite_rows(head_dim))):
         q_ref, s_ref = quantize_int4_groupwise(x, group_size=32)
         p_ref = pack_int4(q_ref)
         xg = x.to(device)

@@ -222,3 +222,30 @@ def test_append_torch_and_c_agree_on_kat_case():
     c_append(b)
     for name in ("k_data", "v_data", "k_scale", "v_scale"):
         assert torch.equal(a[name].view(torch.uint8), b[name].view(torch.uint8))
+
+
+def test_quantize_non_finite_groups_follow_torch():
+    # torch_eager_kv.py:69-86 on non-finite input: amax and clamp_min keep
+    # NaN, so a NaN group's scale is NaN (stored by torch as 0x7E00 whatever
+    # the payload) and an infinite group's is inf; x / scale is then +-0 or
+    # NaN, which round/clamp keep and float -> int8 turns into 0.  Pinned
+    # against torch's own ops on plain tensors, not against the oracle's code.
+    from oracle.torch_eager_kv import quantize_int4_groupwise
+
+    x = torch.randn(4, 64).to(torch.float16)
+    x[0, 3] = float("nan")
+    x[1, 40] = float("inf")
+    x[2, 0] = -float("inf")
+    x[2, 1] = float("nan")
+    x[3, 33] = torch.tensor(0x7D01, dtype=torch.int16).view(torch.float16)  # a signalling-NaN payload
+    q, s = quantize_int4_groupwise(x, 32)
+    sb = s.view(torch.int16)
+    assert sb[0, 0].item() == 0x7E00 and sb[1, 1].item() == 0x7C00
+    assert sb[2, 0].item() == 0x7E00 and sb[3, 1].item() == 0x7E00
+    assert not q[0, :32].any() and not q[1, 32:].any() and not q[2, :32].any() and not q[3, 32:].any()
+    # the finite groups are untouched by their neighbours
+    assert torch.isfinite(s[0, 1].float()) and torch.isfinite(s[1, 0].float())
+    # the same values straight from torch's ops
+    nan_group = torch.full((32,), float("nan"))
+    assert torch.round(nan_group / nan_group).clamp(-7, 7).to(torch.int8).eq(0).all()
+    assert (nan_group.abs().amax() / 7.0).clamp_min(2.0 ** -14).to(torch.float16).view(torch.int16).item() == 0x7E00
