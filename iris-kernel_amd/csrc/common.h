@@ -72,19 +72,17 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expect) 
 // LDS a workgroup may use on gfx950 (per CU).
 constexpr int kMaxLdsBytes = 160 * 1024;
 
-// Lets KERNEL take up to kMaxLdsBytes of dynamic LDS on the current device
-// (HIP's default limit is 64 KiB).  Done once per device, remembered in an
-// atomic bitmask, so concurrent launches from several host threads are safe:
-// two threads racing here both set the same (idempotent) attribute.
-template <auto KERNEL>
-inline int allow_full_lds() {
-    static std::atomic<uint64_t> done{0};
+// Lets `kernel` take up to kMaxLdsBytes of dynamic LDS on the current device
+// (HIP's default limit is 64 KiB).  Done once per device, remembered in the
+// caller's atomic bitmask (one per kernel), so concurrent launches from
+// several host threads are safe: two threads racing here both set the same
+// (idempotent) attribute.
+inline int allow_full_lds(const void* kernel, std::atomic<uint64_t>& done) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return kLaunchError;
     const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
     if (bit != 0 && (done.load(std::memory_order_acquire) & bit)) return kOk;
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(KERNEL), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            kMaxLdsBytes) != hipSuccess)
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytes) != hipSuccess)
         return kLaunchError;
     done.fetch_or(bit, std::memory_order_release);
     return kOk;

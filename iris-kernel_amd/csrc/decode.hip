@@ -861,7 +861,9 @@ static int pick_kvw(int g, int hkv, int64_t batch, int64_t max_pages) {
 template <int D, int KVW>
 static int lds_bytes(int nw) {
     const int bytes = DecodeLayout<D, KVW>::WAVE_LDS * nw;
-    if (bytes > 65536 && allow_full_lds<&int4_decode_kernel<D, KVW>>() != kOk) return -1;
+    static std::atomic<uint64_t> lds_raised{0};
+    if (bytes > 65536 && allow_full_lds(reinterpret_cast<const void*>(&int4_decode_kernel<D, KVW>), lds_raised) != kOk)
+        return -1;
     return bytes;
 }
 

@@ -65,8 +65,12 @@
 // * fp32 online softmax in base 2 with lazy rescaling (p <= 4).
 #include <type_traits>
 
+#include <stdlib.h>
+#include <string.h>
+
 #include "common.h"
 #include "decode_pages.h"
+#include "decode_stream.h"
 #include "iris_hip.h"
 
 namespace iris {
@@ -985,6 +989,11 @@ namespace {
 
 constexpr int kWaves = 16;  // every (Hkv, head_dim) layout runs 16 waves per workgroup
 
+bool stream_allowed() {
+    const char* sel = getenv("IRIS_DECODE_KERNEL");
+    return sel == nullptr || strcmp(sel, "pages") != 0;
+}
+
 // Scale slots per query head: as many of the G groups as fit beside the
 // group's query heads in the 16 MFMA columns.
 int pick_gs(int g, int head_dim) {
@@ -1044,7 +1053,10 @@ WorkspaceLayout workspace_layout(int64_t batch, int64_t num_q_heads, int64_t hea
 template <int D, int GS, int HKV>
 int launch(dim3 grid, int lds, hipStream_t s, const pg::Args& a) {
     static_assert(pg::page_geom(HKV, D).nw == kWaves, "16 waves per workgroup");
-    if (lds > 65536 && allow_full_lds<&pg::int4_decode_pages_kernel<D, GS, HKV>>() != kOk) return kLaunchError;
+    static std::atomic<uint64_t> lds_raised{0};
+    if (lds > 65536 &&
+        allow_full_lds(reinterpret_cast<const void*>(&pg::int4_decode_pages_kernel<D, GS, HKV>), lds_raised) != kOk)
+        return kLaunchError;
     hipLaunchKernelGGL((pg::int4_decode_pages_kernel<D, GS, HKV>), grid, dim3(64 * kWaves), lds, s, a);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchError;
 }
@@ -1159,6 +1171,14 @@ int pages_launch(const void* query, const void* k_data, const void* v_data, cons
     const bool balanced = chunk_tiles < 0;
     const int64_t share = balanced ? -(int64_t)chunk_tiles : chunk_tiles;
     if (share <= 0 || share > pg::kMaxChunkTiles || max_chunks <= 0) return kInvalidArgument;
+    // Chunk mode of the shapes the streaming kernel has (decode_stream.hip):
+    // it runs them instead (IRIS_DECODE_KERNEL=pages keeps this kernel, for
+    // A/B measurements).  Its workspace is no larger than this kernel's.
+    if (!balanced && stream_supported(num_q_heads, num_kv_heads, head_dim) && max_chunks <= stream_max_chunks() &&
+        stream_allowed())
+        return stream_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
+                             workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, max_pages,
+                             softmax_scale, chunk_tiles, max_chunks, stream);
     if (!balanced && share * max_chunks * 2 < max_pages) return kInvalidArgument;
     if (balanced && max_chunks > 8 * pg::kMaxGroups) return kInvalidArgument;
     const int g = (int)(num_q_heads / num_kv_heads);

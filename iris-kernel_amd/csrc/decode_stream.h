@@ -1,0 +1,30 @@
+// Host entry points of the streaming decode kernel (decode_stream.hip),
+// called by the C ABI in decode.hip / decode_pages.hip for the shapes it
+// supports.
+#pragma once
+
+#include <stdint.h>
+
+#define IRIS_INTERNAL __attribute__((visibility("hidden")))
+
+namespace iris {
+
+// head_dim 128, 8 kv heads, 4 query heads per kv head.
+IRIS_INTERNAL bool stream_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim);
+
+// Most chunks per sequence a launch can merge.
+IRIS_INTERNAL int stream_max_chunks();
+
+// Split-KV workspace of a launch with max_chunks chunks per sequence.
+IRIS_INTERNAL int64_t stream_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim,
+                                             int64_t max_chunks);
+
+// Chunk-mode launch: batch x max_chunks workgroups of chunk_tiles 32-token tiles.
+IRIS_INTERNAL int stream_launch(const void* query, const void* k_data, const void* v_data, const void* k_scale,
+                                const void* v_scale, const int32_t* block_table, const int32_t* seq_lens,
+                                void* output, int32_t output_is_f32, void* workspace, int64_t workspace_bytes_avail,
+                                int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                int64_t max_pages, float softmax_scale, int32_t chunk_tiles, int32_t max_chunks,
+                                void* stream);
+
+}  // namespace iris

@@ -1,0 +1,794 @@
+// INT4 paged decode attention for gfx950 (MI355X): the streaming kernel.
+//
+// Replaces the TileLang kernel `_int4_paged_decode_attention`
+// (src/iris_kernel/fused_attention.py:11-220 in Hunter2030ZeRo/Iris-Kernel)
+// for head_dim 128, 4 query heads per kv head and 8 kv heads (the GQA shape
+// of Llama-3-8B and its relatives); it computes the result of
+// `torch_eager_int4_paged_decode_attention`
+// (src/iris_kernel/torch_eager_attention.py:154-239).
+//
+// Streaming
+// ---------
+// HBM serves this cache best as whole pages read by one CU (a page of all 8
+// kv heads is an 8 KiB slab per tensor): 151 MB of random 8 KiB pages plus
+// their scales stream in 23.6 us on MI355X with 16 waves a CU and two or
+// three 1 KiB loads in flight per wave, while 128- or 256-byte head slices
+// read by different CUs take 25.7-27.8 us and deeper queues 26-27 us.  So:
+// * a workgroup of 16 waves owns (sequence, chunk of 32-token tiles) and
+//   reads every kv head of each page;
+// * every load moves 1 KiB straight into LDS (buffer_load ... lds);
+// * a ring of four slots, three in flight.  Slot s holds the K pages and K
+//   scales of tile s and the V pages and V scales of tile s - 1 (36 loads:
+//   each wave one K and one V load, waves 0-3 one scale load each).
+//
+// Compute: two wave sets, one barrier per step
+// --------------------------------------------
+// Wave w works on kv head w % 8 for the tiles of parity w / 8.  A tile is
+// computed in two halves on consecutive steps: the first half (QK and the
+// row maxima) on step s reads the K half of slot s; the second (online
+// softmax update and PV) on step s + 1 reads the V half of slot s + 1.  On
+// every step one set runs first halves and the other set second halves, so
+// all 16 waves compute while three slots stream in; the step's barrier both
+// publishes slot s and frees slot s - 1 for tile s + 3.
+// * QK with the query as the MFMA A operand and K as B
+//   (v_mfma_f32_16x16x32_f16): A row (h, g) = query head h, scale group g;
+//   a lane of k-chunk jq holds 32 dims of group jq, and A row (h, g) is
+//   zero unless g == jq, so C row (h, g) sums group g only.  C lane (token
+//   column n, jq) then holds the 4 groups of head jq for one token: the K
+//   scale (per token and group) is applied in the lane and the score is
+//   4 FMAs, with no cross-lane sum.
+// * Codes enter the MFMA as exact fp16 subnormals (nibble + 8), the offset
+//   removed by the accumulator's initial value (Q side) and by a running sum
+//   of the PV weights (V side).
+// * Two MFMA chains per tile, columns n -> tokens T_e(n) = 16 (n >> 3) +
+//   4 ((n & 7) >> 1) + (n & 1) + 2 e, so a lane's two scores are tokens t
+//   and t + 2, adjacent in the PV operand order below.
+// * fp32 online softmax in base 2 with lazy rescaling: a head's 32 scores
+//   sit in one 16-lane row (2 per lane); the row maximum is 4 DPP steps.
+// * PV with V as the B operand (transposed reads, ds_read_b64_tr_b8) and
+//   A row (h, g) = p[h, t] * v_scale[t, g] rounded once to fp16, moved into
+//   the A layout through a per-kv-head LDS area (4 dword writes, one 16-byte
+//   read).  A PV MFMA covers 16 dims of one group; its C rows (h, g) are
+//   kept, the others discarded.
+// * The two sets' softmax states of a kv head are combined in the epilogue.
+//
+// Split-KV: sequences longer than one chunk publish (m, l, o / l) per query
+// head; the last chunk to arrive merges them in the same launch.
+#include "common.h"
+#include "decode_stream.h"
+#include "iris_hip.h"
+
+namespace iris {
+namespace st {
+
+constexpr int kTile = 32;
+constexpr int kPage = 16;
+constexpr int kWaves = 16;
+constexpr int kSlots = 4;           // ring slots
+constexpr int kAhead = kSlots - 1;  // slots in flight
+constexpr int kJobs = 3;            // loads per wave per slot
+constexpr int kMaxChunkTiles = 64;  // a chunk's 128 page ids fill two VGPRs
+constexpr int kMaxChunks = 64;      // partials the merge reads
+constexpr int kMergeBatch = 8;      // partials in flight per thread in the merge
+constexpr float kLazy = 2.0f;       // rescale when a row maximum grows by more (base 2)
+constexpr int kSC1 = 16;            // cache-policy bit sc1: device-coherent access
+constexpr int kNT = 2;              // cache-policy bit nt: streaming
+
+typedef int int2v_t __attribute__((ext_vector_type(2)));
+typedef float float2v_t __attribute__((ext_vector_type(2)));
+#define IRIS_LDS __attribute__((address_space(3)))
+
+// Geometry of the supported shape: head_dim 128 (4 scale groups), 4 query
+// heads per kv head, HKV kv heads.
+template <int HKV>
+struct Geo {
+    static constexpr int D = 128, G = 4, GQ = 4;
+    static constexpr int CK = HKV * 4;           // 16-byte chunks per token row of K or V data
+    static constexpr int KPAGE = 16 * HKV * 64;  // data bytes of a page (per tensor)
+    static constexpr int SPAGE = 16 * HKV * 8;   // scale bytes of a page (per tensor)
+    // Slot, in load order: [K p0][K p1][V p0][V p1][KS p0][KS p1][VS p0][VS p1]
+    // (K of tile s, V of tile s - 1).
+    static constexpr int K_OFF = 0, V_OFF = 2 * KPAGE, KS_OFF = 4 * KPAGE, VS_OFF = 4 * KPAGE + 2 * SPAGE;
+    static constexpr int SLOT = 4 * KPAGE + 4 * SPAGE;
+    // Per-kv-head P areas after the ring (the two waves of a kv head run
+    // their PV halves on alternate steps): 16 rows (h, g) of 32 halves,
+    // padded to 80 bytes so the writes and the 16-byte reads are free of
+    // bank conflicts.
+    static constexpr int P_ROW = 80, P_AREA = 16 * P_ROW, P_OFF = kSlots * SLOT;
+    // The empty scale-load slot of waves 4-15 writes (zeros) here.
+    static constexpr int SINK_OFF = P_OFF + HKV * P_AREA;
+    static constexpr int EPI_AREA = (8 + GQ * D) * 4;  // one set's (m, l, o) of a kv head in the epilogue
+    static constexpr int LDS_MAIN = SINK_OFF + 1024;
+};
+
+struct Args {
+    const half_t* q;
+    const uint8_t* k_data;
+    const uint8_t* v_data;
+    const uint8_t* k_scale;
+    const uint8_t* v_scale;
+    const int32_t* block_table;
+    const int32_t* seq_lens;
+    void* out;
+    uint32_t* counters;  // counter of sequence b at b * kCountersPerSeq; zero between calls
+    float* part_o;       // [B][max_chunks][Hq][D] o / l of each chunk
+    float* part_ml;      // [B][max_chunks][Hq][2] (m, l), base-2 logits
+    int out_f32;
+    int batch, n_q_heads, max_pages, max_chunks, chunk_tiles;
+    float log2_scale;
+};
+
+// ---------------------------------------------------------------- operands
+
+// K operand: eight codes (one dword, low nibble first) -> fp16 subnormals in
+// the order d0, d4, 16*d1, 16*d5, d2, d6, 16*d3, 16*d7 (units of 2^-24,
+// codes offset by +8).  Each half is one v_bitop3 ((x ^ c) & m).
+__device__ __forceinline__ half8_t k_operand(uint32_t x) {
+    const uint32_t y = x >> 8;
+    const u32x4_t r = {(x ^ 0x00080008u) & 0x000F000Fu, (x ^ 0x00800080u) & 0x00F000F0u,
+                       (y ^ 0x00080008u) & 0x000F000Fu, (y ^ 0x00800080u) & 0x00F000F0u};
+    return __builtin_bit_cast(half8_t, r);
+}
+
+// q (8 consecutive dims) in the order of k_operand, high-nibble dims / 16.
+__device__ __forceinline__ half8_t q_operand(u32x4_t w) {
+    const half2_t w0 = as_half2(w[0]), w1 = as_half2(w[1]), w2 = as_half2(w[2]), w3 = as_half2(w[3]);
+    const half_t s16 = (half_t)0.0625f;
+    return half8_t{w0.x, w2.x, w0.y * s16, w2.y * s16, w1.x, w3.x, w1.y * s16, w3.y * s16};
+}
+
+// V operands from the 8 bytes of one transposed read (8 tokens of one byte
+// column): lo = low nibbles (even dim), hi = 16 * high nibbles (odd dim),
+// both in the k-slot order of the read (slot s = token 16 r + 4 jq + i with
+// 4 r + i = kVSlotByte[s]).
+__device__ __forceinline__ void v_operands(int2v_t w, half8_t& lo, half8_t& hi) {
+    const uint32_t a = (uint32_t)w[0], b = (uint32_t)w[1];
+    const uint32_t a8 = a >> 8, b8 = b >> 8;
+    const u32x4_t l = {(a ^ 0x00080008u) & 0x000F000Fu, (a8 ^ 0x00080008u) & 0x000F000Fu,
+                       (b ^ 0x00080008u) & 0x000F000Fu, (b8 ^ 0x00080008u) & 0x000F000Fu};
+    const u32x4_t h = {(a ^ 0x00800080u) & 0x00F000F0u, (a8 ^ 0x00800080u) & 0x00F000F0u,
+                       (b ^ 0x00800080u) & 0x00F000F0u, (b8 ^ 0x00800080u) & 0x00F000F0u};
+    lo = __builtin_bit_cast(half8_t, l);
+    hi = __builtin_bit_cast(half8_t, h);
+}
+
+__device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Maximum / sum over the 16 lanes of a row (DPP: xor 1, xor 2, then the
+// half-row and row mirrors).
+__device__ __forceinline__ float dpp_f(float x, int ctrl) {
+    switch (ctrl) {
+        case 0: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true));
+        case 1: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true));
+        case 2: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true));
+        default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, true));
+    }
+}
+// Row maximum as four fused DPP maxima (v_max_f32_dpp; a VGPR a VALU
+// instruction wrote is read through DPP two wait states later).  NaN
+// operands follow v_max_f32: the other operand is returned.
+__device__ __forceinline__ float row16_max(float x) {
+    float y;
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=&v"(y)
+        : "v"(x));
+    return y;
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f(x, 0);
+    x += dpp_f(x, 1);
+    x += dpp_f(x, 2);
+    return x + dpp_f(x, 3);
+}
+
+// Consecutive logical workgroup ids (the chunks of one sequence) on one XCD.
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+    constexpr int kXcds = 8;
+    if (nblocks % kXcds != 0) return bid;
+    return (bid % kXcds) * (nblocks / kXcds) + bid / kXcds;
+}
+
+__device__ __forceinline__ uint32_t opaque(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const IRIS_LDS void*)p;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Reads of tile data, which direct-to-LDS loads wrote, are inline assembly
+// waiting for their own results: the compiler cannot tell them from the
+// loads still streaming into the other buffers and would wait for those too.
+// A vmcnt wait and a workgroup barrier precede every such read.
+__device__ __forceinline__ void lds_tile_reads(uint32_t k0, uint32_t k1, uint32_t ks0, uint32_t ks1, u32x4_t& kq0,
+                                               u32x4_t& kq1, u32x2_t& ksc0, u32x2_t& ksc1) {
+    asm volatile(
+        "ds_read_b128 %0, %4\n\t"
+        "ds_read_b128 %1, %5\n\t"
+        "ds_read_b64 %2, %6\n\t"
+        "ds_read_b64 %3, %7\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(kq0), "=&v"(kq1), "=&v"(ksc0), "=&v"(ksc1)
+        : "v"(k0), "v"(k1), "v"(ks0), "v"(ks1)
+        : "memory");
+}
+__device__ __forceinline__ void lds_v_reads(uint32_t vs0, uint32_t vs1, const uint32_t (&tr)[4], u32x2_t& vsc0,
+                                            u32x2_t& vsc1, int2v_t (&w)[4]) {
+    asm volatile(
+        "ds_read_b64 %0, %6\n\t"
+        "ds_read_b64 %1, %7\n\t"
+        "ds_read_b64_tr_b8 %2, %8\n\t"
+        "ds_read_b64_tr_b8 %3, %9\n\t"
+        "ds_read_b64_tr_b8 %4, %10\n\t"
+        "ds_read_b64_tr_b8 %5, %11\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(vsc0), "=&v"(vsc1), "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
+        : "v"(vs0), "v"(vs1), "v"(tr[0]), "v"(tr[1]), "v"(tr[2]), "v"(tr[3])
+        : "memory");
+}
+// The kv head's P area: four dword writes (rows of groups 0-3, 80 bytes
+// apart), then the 16-byte read of the A operand (same wave, so the writes
+// are complete when the read runs).
+__device__ __forceinline__ u32x4_t lds_p_transpose(uint32_t wr, const uint32_t (&pw)[4], uint32_t rd) {
+    u32x4_t a;
+    asm volatile(
+        "ds_write_b32 %1, %2\n\t"
+        "ds_write_b32 %1, %3 offset:80\n\t"
+        "ds_write_b32 %1, %4 offset:160\n\t"
+        "ds_write_b32 %1, %5 offset:240\n\t"
+        "s_waitcnt lgkmcnt(0)\n\t"
+        "ds_read_b128 %0, %6\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(a)
+        : "v"(wr), "v"(pw[0]), "v"(pw[1]), "v"(pw[2]), "v"(pw[3]), "v"(rd)
+        : "memory");
+    return a;
+}
+
+// Position swizzles of a page's 16-byte chunks in LDS (row = token row of
+// the page, r = page within the tile, CK chunks per row):
+// * K: chunk c of row `row` sits at position c ^ kkey(row, r), so the 16
+//   lanes of one k-chunk (8 rows of each page) read 16 different bank
+//   groups;
+// * V: chunk c of tile token t (0..31) at c ^ vswz(t): a transposed read
+//   over tokens of both pages hits every bank once;
+// * scales: chunk (row, col) at column col ^ ((row >> 2) & 3).
+__device__ __forceinline__ int kkey(int row, int r) { return (row ^ (r << 1)) & 15; }
+template <int CK>
+__device__ __forceinline__ int vswz(int t) { return ((t & 15) ^ (((t >> 4) & 1) * (CK / 2))) & (CK - 1); }
+
+__device__ __forceinline__ float4_t load4_sc1(const __amdgpu_buffer_rsrc_t& rs, uint32_t off) {
+    return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kSC1));
+}
+__device__ __forceinline__ float2v_t load2_sc1(const __amdgpu_buffer_rsrc_t& rs, uint32_t off) {
+    return __builtin_bit_cast(float2v_t, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kSC1));
+}
+__device__ __forceinline__ void store4_sc1(float4_t v, const __amdgpu_buffer_rsrc_t& rs, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), rs, off, 0, kSC1);
+}
+__device__ __forceinline__ void store2_sc1(float2v_t v, const __amdgpu_buffer_rsrc_t& rs, uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), rs, off, 0, kSC1);
+}
+
+template <int HKV>
+__global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(Args a) {
+    using L = Geo<HKV>;
+    constexpr int D = L::D, GQ = L::GQ, G = L::G, CK = L::CK, SLOT = L::SLOT;
+    constexpr uint32_t KPAGE = L::KPAGE, SPAGE = L::SPAGE;
+    constexpr int PER_PAGE = L::KPAGE / 1024;  // 1 KiB loads per page of one tensor
+    static_assert(kWaves == 2 * HKV && 2 * PER_PAGE == kWaves, "one K and one V load of each slot per wave");
+    static_assert(L::SPAGE == 1024 && kJobs == 3, "four 1 KiB scale loads per slot, waves 0-3");
+    static_assert(L::P_ROW == 80, "lds_p_transpose writes rows 80 bytes apart");
+    static_assert(L::LDS_MAIN <= 160 * 1024, "LDS of a CU");
+    extern __shared__ __align__(16) uint8_t smem[];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 15;   // MFMA row (A) or column (B, C)
+    const int jq = lane >> 4;  // MFMA k-chunk (A, B) or row quad (C)
+    const int kvh = wave % HKV, par = wave / HKV;  // kv head; tiles of this parity
+
+    const int wg = xcd_remap(blockIdx.x, gridDim.x);
+    const int b = wg / a.max_chunks, chunk = wg % a.max_chunks;
+    const int seq_len = a.seq_lens[b];
+    const int n_tiles = (seq_len + kTile - 1) / kTile;
+    const int t_begin = chunk * a.chunk_tiles;
+    if (t_begin >= n_tiles) return;  // uniform over the workgroup
+    const int t_end = min(t_begin + a.chunk_tiles, n_tiles);
+    const int n_stages = t_end - t_begin;
+    const int n_chunks = (n_tiles + a.chunk_tiles - 1) / a.chunk_tiles;
+    const int p0 = 2 * t_begin;
+    const int last_lp = (seq_len + kPage - 1) / kPage - 1;
+
+    // ---- page ids of the chunk (logical page p0 + i in lane i of pid0 /
+    // pid1), then the raw query rows, both in flight together.
+    const int32_t* bt = a.block_table + (int64_t)b * a.max_pages;
+    int pid0 = 0, pid1 = 0;
+    if (p0 + lane < a.max_pages) pid0 = bt[p0 + lane];
+    if (p0 + 64 + lane < a.max_pages) pid1 = bt[p0 + 64 + lane];
+    // Query A operand: row n = (h, g) = (n >> 2, n & 3), nonzero only where
+    // g == jq: 32 dims of group jq of head h.
+    const half_t* qh = a.q + ((int64_t)b * a.n_q_heads + kvh * GQ) * D;
+    u32x4_t qraw[4];
+    {
+        const bool mine = (n & 3) == jq;
+        const half_t* qrow = qh + (n >> 2) * D + 32 * jq;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            qraw[m] = u32x4_t{0, 0, 0, 0};
+            if (mine) qraw[m] = *reinterpret_cast<const u32x4_t*>(qrow + 8 * m);
+        }
+    }
+
+    // ---- this wave's three loads of a slot (the same every step); each
+    // fills 1 KiB of the slot, its lanes fetching the page chunks the
+    // swizzles put there:
+    // * K piece `wave` of tile s: page kr, token rows 2 qq and 2 qq + 1;
+    // * V piece `wave` of tile s - 1, the same rows;
+    // * waves 0-3: scales KS p0, KS p1 (tile s), VS p0, VS p1 (tile s - 1);
+    //   waves 4-15: an empty load into the sink.
+    const int kr = wave / PER_PAGE, qq = wave % PER_PAGE;
+    uint32_t k_voff, v_voff, s_voff;
+    {
+        const int P = qq * 64 + lane, row = P / CK, cpos = P % CK;
+        k_voff = (uint32_t)(row * CK + (cpos ^ kkey(row, kr))) * 16;
+        v_voff = (uint32_t)(row * CK + (cpos ^ vswz<CK>(16 * kr + row))) * 16;
+        const int srow = lane >> 2, scol = lane & 3;
+        s_voff = (uint32_t)(srow * 64 + ((scol ^ ((srow >> 2) & 3)) * 16));
+    }
+    const bool s_job = wave < 4;
+    const bool s_is_v = (wave & 2) != 0;
+    const int s_r = wave & 1;
+
+    // Physical page of logical page lp (past the sequence: its last page).
+    auto page_of = [&](int lp) -> int64_t {
+        const int rel = min(lp, last_lp) - p0;
+        return (int64_t)__builtin_amdgcn_readlane(rel < 64 ? pid0 : pid1, rel & 63);
+    };
+    pid0 = (int)opaque((uint32_t)pid0);
+    pid1 = (int)opaque((uint32_t)pid1);
+
+    // Slot of step s: K of tile s, V of tile s - 1.  Halves outside the
+    // chunk load with zero-size descriptors (no memory access; the load still
+    // writes zeros into its LDS bytes), so every wave has kJobs loads of every
+    // slot in flight.
+    auto issue = [&](int s) __attribute__((always_inline)) {
+        uint8_t* const dst = smem + (s & (kSlots - 1)) * SLOT;
+        const bool kv = s < n_stages;
+        const bool vv = s >= 1 && s <= n_stages;
+        const int64_t kp = kv ? page_of(2 * (t_begin + s) + kr) : 0;
+        const int64_t vp = vv ? page_of(2 * (t_begin + s - 1) + kr) : 0;
+        const bool sv = s_job && (s_is_v ? vv : kv);
+        const int64_t sp = sv ? page_of(2 * (t_begin + s - (s_is_v ? 1 : 0)) + s_r) : 0;
+        // (the page sizes are the kernel-scope constants: L::KPAGE named in
+        // these descriptor expressions makes clang drop the kernel's host
+        // launch stub)
+        const auto krs = buf_rsrc(a.k_data + kp * KPAGE, kv ? KPAGE : 0u);
+        const auto vrs = buf_rsrc(a.v_data + vp * KPAGE, vv ? KPAGE : 0u);
+        const auto srs = buf_rsrc((s_is_v ? a.v_scale : a.k_scale) + sp * SPAGE, sv ? SPAGE : 0u);
+        uint8_t* const kdst = dst + L::K_OFF + 1024 * wave;
+        uint8_t* const vdst = dst + L::V_OFF + 1024 * wave;
+        uint8_t* const sdst = s_job ? dst + L::KS_OFF + 1024 * wave : smem + L::SINK_OFF;
+        const uint32_t ko = k_voff, vo = v_voff, so = s_voff;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (IRIS_LDS void*)kdst, 16, ko, 0, 0, kNT);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (IRIS_LDS void*)vdst, 16, vo, 0, 0, kNT);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (IRIS_LDS void*)sdst, 16, so, 0, 0, kNT);
+    };
+    // The first three slots stream in while the query operands are prepared.
+#pragma unroll
+    for (int s = 0; s < kAhead; ++s) issue(s);
+
+    half8_t qa[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) qa[m] = q_operand(qraw[m]);
+    // Accumulator start that removes the +8 of the K codes: C row (h, g)
+    // gets -8 * 2^-24 * (sum of q over group g of head h, as the A operand
+    // holds it, high-nibble dims / 16 counted 16 times).  Lane (4 h + g, g)
+    // holds that group in qa; C lane (n, jq) needs rows (jq, 0..3).
+    float4_t init;
+    {
+        float part = 0.0f;
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) part += (float)qa[m][i] * ((i & 2) ? 16.0f : 1.0f);
+        part *= -8.0f * 5.9604644775390625e-08f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            init[g] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                   4 * (16 * g + 4 * jq + g), __builtin_bit_cast(int, part)));
+    }
+
+    // ---- per-lane LDS offsets within a slot
+    // K operand of chain e: token T = 16 (n >> 3) + 4 ((n & 7) >> 1) + (n & 1) + 2 e,
+    // 16 bytes = dims [32 jq, 32 jq + 32) of head kvh.
+    const int T0 = 16 * (n >> 3) + 4 * ((n & 7) >> 1) + (n & 1);
+    uint32_t k_off[2], ks_off[2], vs_off[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int T = T0 + 2 * e;
+        const int r = T >> 4, row = T & 15;
+        k_off[e] = (uint32_t)(L::K_OFF + r * L::KPAGE + (row * CK + ((kvh * 4 + jq) ^ kkey(row, r))) * 16);
+        const int srow = row * 64 + (((kvh >> 1) ^ ((row >> 2) & 3)) * 16) + (kvh & 1) * 8;
+        ks_off[e] = (uint32_t)(L::KS_OFF + r * L::SPAGE + srow);
+        vs_off[e] = (uint32_t)(L::VS_OFF + r * L::SPAGE + srow);
+    }
+    // Transposed V reads of group g: lane (n, jq) points at token tr_tok's
+    // 8-byte half (n & 1) of group g's chunk; after the 8 x 8 byte transpose
+    // it holds byte column n of 8 tokens (k-slot order of v_operands).
+    uint32_t tr_off[G];
+    {
+        const int trk = n >> 1;
+        const int tr_tok = 4 * jq + (trk & 3) + 16 * (trk >> 2);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+            tr_off[g] = (uint32_t)(L::V_OFF + (tr_tok >> 4) * L::KPAGE +
+                                   ((tr_tok & 15) * CK + ((kvh * 4 + g) ^ vswz<CK>(tr_tok))) * 16 + 8 * (n & 1));
+    }
+    // P area of the kv head: row (h, g) = 4 h + g, 32 halves in k-slot order
+    // of the tile's token blocks (block jq' = tokens 4 jq' + i of both
+    // pages).  Lane (n, jq) writes tokens T0 and T0 + 2, k-slots
+    // 4 (n >> 3) + 2 (n & 1) and the next, of block (n & 7) >> 1 in rows
+    // (jq, 0..3); it reads row n, block jq (rows (h, g) feed the PV of group
+    // g only: the other groups' rows carry the wrong V scale and their C rows
+    // are discarded).
+    const uint32_t p_base = lds_addr(smem + L::P_OFF + kvh * L::P_AREA);
+    const uint32_t p_wr =
+        p_base + (uint32_t)((jq * 4) * L::P_ROW + (((n & 7) >> 1) * 8 + 4 * (n >> 3) + 2 * (n & 1)) * 2);
+    const uint32_t p_rd = p_base + (uint32_t)(n * L::P_ROW + jq * 16);
+
+    const float c24 = a.log2_scale * 16777216.0f;  // MFMA units -> base-2 logits
+    float m_run = -INFINITY;                       // row maximum, base-2 logits
+    float l_part = 0.0f;
+    float ps[G];  // sums of the PV weights per group (V code offset)
+    float4_t o[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        ps[g] = 0.0f;
+        o[g][0] = o[g][1] = float4_t{0, 0, 0, 0};
+    }
+    float t[2];     // scores (base-2 logits) of tokens T0, T0 + 2: first half -> second half
+    float mx = 0.0f;  // their row maximum
+
+    // First half of tile `stage` (K half of its slot): scores of the lane's
+    // two tokens and the row maximum.  The two QK chains are interleaved.
+    auto first_half = [&](int stage, uint32_t base) __attribute__((always_inline)) {
+        const int tok0 = (t_begin + stage) * kTile;
+        u32x4_t kq[2];
+        u32x2_t ksc[2];
+        lds_tile_reads(base + k_off[0], base + k_off[1], base + ks_off[0], base + ks_off[1], kq[0], kq[1], ksc[0],
+                       ksc[1]);
+        float4_t acc[2] = {init, init};
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+            for (int m = 0; m < 4; ++m) acc[e] = mfma16x16x32(qa[m], k_operand(kq[e][m]), acc[e]);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const half2_t k01 = as_half2(ksc[e][0]), k23 = as_half2(ksc[e][1]);
+            float s = (float)k01.x * acc[e][0];
+            s = __builtin_fmaf((float)k01.y, acc[e][1], s);
+            s = __builtin_fmaf((float)k23.x, acc[e][2], s);
+            s = __builtin_fmaf((float)k23.y, acc[e][3], s);
+            t[e] = s * c24;
+        }
+        if (tok0 + kTile > seq_len) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+                if (tok0 + T0 + 2 * e >= seq_len) t[e] = -INFINITY;
+        }
+        // row jq = head jq; its maximum is finite (token tok0 < seq_len)
+        mx = row16_max(__builtin_elementwise_maximum(t[0], t[1]));
+    };
+
+    // Second half of tile `stage` (V half of the next slot): online softmax
+    // (lazy rescale), PV weights w = p * v_scale (one fp16 rounding), tokens
+    // T0 and T0 + 2 packed per group, and the PV products.
+    auto second_half = [&](int stage, uint32_t base) __attribute__((always_inline)) {
+        const int tok0 = (t_begin + stage) * kTile;
+        u32x2_t vsc[2];
+        int2v_t vw[G];
+        uint32_t tra[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) tra[g] = base + tr_off[g];
+        lds_v_reads(base + vs_off[0], base + vs_off[1], tra, vsc[0], vsc[1], vw);
+        if (__ballot(mx > m_run + kLazy) != 0) {
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_part *= alpha;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                ps[g] *= alpha;
+                o[g][0] *= alpha;
+                o[g][1] *= alpha;
+            }
+        }
+        float p[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            p[e] = __builtin_amdgcn_exp2f(t[e] - m_run);
+            l_part += p[e];
+        }
+        float vs[2][G];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const half2_t v01 = as_half2(vsc[e][0]), v23 = as_half2(vsc[e][1]);
+            vs[e][0] = (float)v01.x;
+            vs[e][1] = (float)v01.y;
+            vs[e][2] = (float)v23.x;
+            vs[e][3] = (float)v23.y;
+        }
+        // tokens past seq_len: p is 0, and their scale may be anything (NaN included)
+        if (tok0 + kTile > seq_len) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+                if (tok0 + T0 + 2 * e >= seq_len) vs[e][0] = vs[e][1] = vs[e][2] = vs[e][3] = 0.0f;
+        }
+        uint32_t pw[G];
+        const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const half2_t wp = {(half_t)(p[0] * vs[0][g]), (half_t)(p[1] * vs[1][g])};
+            ps[g] = __builtin_amdgcn_fdot2(wp, one2, ps[g], false);
+            pw[g] = as_u32(wp);
+        }
+        const half8_t pa = __builtin_bit_cast(half8_t, lds_p_transpose(p_wr, pw, p_rd));
+        // group g's 32 dims as byte columns n (even dim lo, odd hi)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            half8_t lo, hi;
+            v_operands(vw[g], lo, hi);
+            o[g][0] = mfma16x16x32(pa, lo, o[g][0]);
+            o[g][1] = mfma16x16x32(pa, hi, o[g][1]);
+        }
+    };
+
+    // ---- the pipeline.  Step s: wait for this wave's loads of slot s (the
+    // slots s + 1, s + 2 stay in flight); the barrier makes every wave's
+    // slot-s loads visible and frees slot s - 1, which receives slot s + 3;
+    // the set of parity s runs the first half of tile s, the other set the
+    // second half of tile s - 1.  Every wave passes the n_stages + 1 steps'
+    // barriers; each set has a loop of its own, two steps per iteration, so
+    // that its halves are straight-line code.
+    auto step = [&](int s) __attribute__((always_inline)) -> uint32_t {
+        wait_vmcnt<(kAhead - 1) * kJobs>();
+        __builtin_amdgcn_s_barrier();
+        issue(s + kAhead);
+        return lds_addr(smem) + (uint32_t)((s & (kSlots - 1)) * SLOT);
+    };
+    if (par == 0) {
+        int s = 0;
+        for (; s < n_stages; s += 2) {
+            first_half(s, step(s));
+            second_half(s, step(s + 1));
+        }
+        if (s == n_stages) step(s);
+    } else {
+        step(0);
+        int s = 1;
+        for (; s < n_stages; s += 2) {
+            first_half(s, step(s));
+            second_half(s, step(s + 1));
+        }
+        if (s == n_stages) step(s);
+    }
+    wait_vmcnt<0>();  // the empty loads past the chunk still write LDS
+    __syncthreads();
+
+    // ---- each set's (m, l, o) of kv head kvh in LDS area `wave`:
+    // [0, 4) m, [4, 8) l, [8 + h D, ...) o (unnormalised, code offset removed).
+    {
+        l_part = row16_sum(l_part);
+        float psr[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) psr[g] = 8.0f * row16_sum(ps[g]);
+        float* const ep = reinterpret_cast<float*>(smem + wave * L::EPI_AREA);
+        if (n == 0) {
+            ep[jq] = m_run;
+            ep[4 + jq] = l_part;
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+                ep[8 + jq * D + 32 * g + 2 * n + e] = o[g][e][g] * (e ? 1048576.0f : 16777216.0f) - psr[g];
+    }
+    __syncthreads();
+
+    // ---- the chunk's result for element idx = (kv head, query head, dim),
+    // 4 dims at a time: the two sets' states combined.  A set without tiles
+    // (a one-tile chunk) has m = -inf, l = 0, o = 0 and weight 0.
+    const int hq = a.n_q_heads;
+    const int total = hq * D, n4 = total / 4;
+    auto chunk4 = [&](int e4, float& m, float& l) -> float4_t {
+        const int idx = 4 * e4;
+        const int j = idx / (GQ * D), rem = idx - j * (GQ * D), h = rem / D, d = rem - h * D;
+        const float* w0 = reinterpret_cast<const float*>(smem + j * L::EPI_AREA);
+        const float* w1 = reinterpret_cast<const float*>(smem + (HKV + j) * L::EPI_AREA);
+        m = fmaxf(w0[h], w1[h]);
+        const float a0 = __builtin_amdgcn_exp2f(w0[h] - m), a1 = __builtin_amdgcn_exp2f(w1[h] - m);
+        l = w0[4 + h] * a0 + w1[4 + h] * a1;
+        const float4_t o0 = *reinterpret_cast<const float4_t*>(w0 + 8 + h * D + d);
+        const float4_t o1 = *reinterpret_cast<const float4_t*>(w1 + 8 + h * D + d);
+        return (o0 * a0 + o1 * a1) * (1.0f / l);
+    };
+    const int64_t out_base = (int64_t)b * total;
+    auto store_out4 = [&](int e4, float4_t v) {
+        if (a.out_f32) {
+            *reinterpret_cast<float4_t*>(reinterpret_cast<float*>(a.out) + out_base + 4 * e4) = v;
+        } else {
+            const half2_t lo = {(half_t)v[0], (half_t)v[1]}, hi = {(half_t)v[2], (half_t)v[3]};
+            *reinterpret_cast<u32x2_t*>(reinterpret_cast<half_t*>(a.out) + out_base + 4 * e4) =
+                u32x2_t{as_u32(lo), as_u32(hi)};
+        }
+    };
+    if (n_chunks == 1) {
+        for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
+            float m, l;
+            store_out4(e4, chunk4(e4, m, l));
+        }
+        return;
+    }
+
+    // ---- split-KV: publish (o / l, m, l) with device-coherent stores; the
+    // last chunk to arrive merges every chunk of the sequence.
+    const uint32_t part_o = (uint32_t)total * 4, part_ml = (uint32_t)hq * 8;  // bytes per partial
+    const int64_t row0 = (int64_t)b * a.max_chunks;
+    {
+        const auto ro = buf_rsrc(a.part_o + (row0 + chunk) * total, part_o);
+        const auto rm = buf_rsrc(a.part_ml + (row0 + chunk) * hq * 2, part_ml);
+        for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
+            float m, l;
+            const float4_t v = chunk4(e4, m, l);
+            store4_sc1(v, ro, (uint32_t)e4 * 16);
+            if ((4 * e4) % D == 0) store2_sc1(float2v_t{m, l}, rm, (uint32_t)(4 * e4 / D) * 8);
+        }
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    uint32_t* const ctl = reinterpret_cast<uint32_t*>(smem + 2 * HKV * L::EPI_AREA);
+    if (threadIdx.x == 0)
+        ctl[0] = arrive_last(a.counters + (int64_t)b * kCountersPerSeq, (uint32_t)n_chunks) ? 1u : 0u;
+    __syncthreads();
+    if (ctl[0] == 0) return;
+
+    // Merge the M = n_chunks partials, each thread a float4 of the output:
+    // o = sum_c w_c (o / l)_c / sum_c w_c with w_c = l_c 2^(m_c - m*), the
+    // partials and their (m, l) loaded together, kMergeBatch chunks at a
+    // time, m* the running maximum.
+    const int M = n_chunks;
+    const auto ro = buf_rsrc(a.part_o + row0 * total, part_o * (uint32_t)M);
+    const auto rm = buf_rsrc(a.part_ml + row0 * hq * 2, part_ml * (uint32_t)M);
+    for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
+        const int h = 4 * e4 / D;
+        float mstar = -INFINITY, lsum = 0.0f;
+        float4_t acc = {0, 0, 0, 0};
+        for (int c0 = 0; c0 < M; c0 += kMergeBatch) {
+            float4_t oc[kMergeBatch];
+            float2v_t ml[kMergeBatch];
+#pragma unroll
+            for (int cb = 0; cb < kMergeBatch; ++cb) {
+                const uint32_t c = (uint32_t)min(c0 + cb, M - 1);
+                oc[cb] = load4_sc1(ro, c * part_o + (uint32_t)e4 * 16);
+                ml[cb] = load2_sc1(rm, (c * (uint32_t)hq + (uint32_t)h) * 8);
+            }
+            // past M: a repeat of partial M - 1 with weight 0
+            float mb = mstar;
+#pragma unroll
+            for (int cb = 0; cb < kMergeBatch; ++cb) mb = fmaxf(mb, ml[cb][0]);
+            const float r = __builtin_amdgcn_exp2f(mstar - mb);  // 0 on the first batch
+            acc *= r;
+            lsum *= r;
+#pragma unroll
+            for (int cb = 0; cb < kMergeBatch; ++cb) {
+                const float w = c0 + cb < M ? ml[cb][1] * __builtin_amdgcn_exp2f(ml[cb][0] - mb) : 0.0f;
+                acc += oc[cb] * w;
+                lsum += w;
+            }
+            mstar = mb;
+        }
+        store_out4(e4, acc * (1.0f / lsum));
+    }
+}
+
+}  // namespace st
+
+// ------------------------------------------------------------------ host side
+
+namespace {
+
+template <int HKV>
+int stream_lds_bytes() {
+    using L = st::Geo<HKV>;
+    const int epi = 2 * HKV * L::EPI_AREA + 16;
+    return L::LDS_MAIN > epi ? L::LDS_MAIN : epi;
+}
+
+template <int HKV>
+int launch_stream(dim3 grid, hipStream_t s, const st::Args& a) {
+    const int lds = stream_lds_bytes<HKV>();
+    if (lds > kMaxLdsBytes) return kInvalidArgument;
+    static std::atomic<uint64_t> lds_raised{0};
+    if (allow_full_lds(reinterpret_cast<const void*>(&st::int4_decode_stream_kernel<HKV>), lds_raised) != kOk)
+        return kLaunchError;
+    hipLaunchKernelGGL((st::int4_decode_stream_kernel<HKV>), grid, dim3(64 * st::kWaves), lds, s, a);
+    return hipGetLastError() == hipSuccess ? kOk : kLaunchError;
+}
+
+}  // namespace
+
+int stream_max_chunks() { return st::kMaxChunks; }
+
+bool stream_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim) {
+    return head_dim == 128 && num_kv_heads == 8 && num_q_heads == 4 * num_kv_heads;
+}
+
+int64_t stream_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t max_chunks) {
+    const int64_t o = batch * max_chunks * num_q_heads * head_dim * 4;
+    return counter_region_bytes(batch) + (o + 255) / 256 * 256 + batch * max_chunks * num_q_heads * 2 * 4;
+}
+
+int stream_launch(const void* query, const void* k_data, const void* v_data, const void* k_scale, const void* v_scale,
+                  const int32_t* block_table, const int32_t* seq_lens, void* output, int32_t output_is_f32,
+                  void* workspace, int64_t workspace_bytes_avail, int64_t batch, int64_t num_q_heads,
+                  int64_t num_kv_heads, int64_t head_dim, int64_t max_pages, float softmax_scale, int32_t chunk_tiles,
+                  int32_t max_chunks, void* stream) {
+    if (!stream_supported(num_q_heads, num_kv_heads, head_dim)) return kInvalidArgument;
+    if (chunk_tiles <= 0 || chunk_tiles > st::kMaxChunkTiles || max_chunks <= 0 || max_chunks > st::kMaxChunks)
+        return kInvalidArgument;
+    if ((int64_t)chunk_tiles * max_chunks * 2 < max_pages) return kInvalidArgument;  // the grid covers every page
+    const int64_t nblocks = batch * (int64_t)max_chunks;
+    if (nblocks > 0x7FFFFFFF) return kInvalidArgument;
+    st::Args a;
+    a.q = (const half_t*)query;
+    a.k_data = (const uint8_t*)k_data;
+    a.v_data = (const uint8_t*)v_data;
+    a.k_scale = (const uint8_t*)k_scale;
+    a.v_scale = (const uint8_t*)v_scale;
+    a.block_table = block_table;
+    a.seq_lens = seq_lens;
+    a.out = output;
+    a.out_f32 = output_is_f32;
+    a.batch = (int)batch;
+    a.n_q_heads = (int)num_q_heads;
+    a.max_pages = (int)max_pages;
+    a.max_chunks = max_chunks;
+    a.chunk_tiles = chunk_tiles;
+    a.log2_scale = softmax_scale * 1.4426950408889634f;
+    a.counters = nullptr;
+    a.part_o = a.part_ml = nullptr;
+    if (max_chunks > 1) {
+        const int64_t need = stream_workspace_bytes(batch, num_q_heads, head_dim, max_chunks);
+        if (workspace == nullptr || workspace_bytes_avail < need) return kWorkspaceTooSmall;
+        uint8_t* const ws = (uint8_t*)workspace;
+        const int64_t o = batch * max_chunks * num_q_heads * head_dim * 4;
+        a.counters = (uint32_t*)ws;
+        a.part_o = (float*)(ws + counter_region_bytes(batch));
+        a.part_ml = (float*)(ws + counter_region_bytes(batch) + (o + 255) / 256 * 256);
+    }
+    return launch_stream<8>(dim3((unsigned)nblocks), (hipStream_t)stream, a);
+}
+
+}  // namespace iris

@@ -28,6 +28,7 @@ SOURCES = {
     "append.hip": ["-ffp-contract=off"],
     "decode.hip": [],
     "decode_pages.hip": [],
+    "decode_stream.hip": [],
     "decode_fp16.hip": [],
     "kv_fp16.hip": ["-ffp-contract=off"],
     "check.hip": [],
