@@ -177,6 +177,29 @@ int iris_int4_paged_decode_attention(const void *query, const void *k_data, cons
                                      int32_t waves_per_block, void *stream);
 
 /*
+ * iris_int4_paged_decode_attention without the workspace arguments.  No
+ * counterpart in the reference (its decode has no split-KV workspace): for
+ * callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  The
+ * split-KV workspace is an 8 MiB array inside the library, one per GPU,
+ * held until the process ends; a plan that needs more returns
+ * IRIS_ERR_WORKSPACE without launching the decode.  The first call on a GPU
+ * looks the array up (hipGetSymbolAddress); a split call whose batch exceeds
+ * the previous split call's first clears the counters of its sequences with
+ * a fill kernel on `stream`.  Every call on a GPU shares that GPU's array:
+ * calls that overlap in time race (issue them on one stream).  Nothing is
+ * allocated.  Other arguments and results as iris_int4_paged_decode_attention.
+ */
+int iris_int4_paged_decode_attention_noalloc(const void *query, const void *k_data, const void *v_data,
+                                             const void *k_scale, const void *v_scale,
+                                             const int32_t *block_table, const int32_t *seq_lens,
+                                             void *output, int32_t output_is_f32, int64_t batch,
+                                             int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                                             int64_t page_size, int64_t num_pages, int64_t max_pages,
+                                             float softmax_scale, int32_t chunk_tiles, int32_t max_chunks,
+                                             int32_t waves_per_block, void *stream);
+
+/*
  * Split plan for iris_fp16_paged_decode_attention (no reference counterpart;
  * see iris_decode_plan): pages per chunk (out_chunk_pages, at most 256),
  * chunks per (sequence, kv head) for the widest block_table

@@ -1065,4 +1065,81 @@ extern "C" int iris_int4_paged_decode_attention(
     return kOk;
 }
 
+// ------------------------------------------------ no-allocation entry point
+
+namespace iris {
+namespace {
+
+// Split-KV workspace of iris_int4_paged_decode_attention_noalloc: one array
+// per GPU (each device holds its own copy, at its own address), kept until
+// the process ends.  Host code uses the address hipGetSymbolAddress returns
+// on that device, never the array's name.
+constexpr int64_t kScratchBytes = 8 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+struct ScratchSlot {
+    std::atomic<uintptr_t> ptr{0};   // device address of `scratch` (0: not looked up yet)
+    std::atomic<int64_t> batch{0};   // batch of the last split call: counters [0, batch) are zero
+};
+ScratchSlot g_scratch[kMaxScratchDevices];
+
+__global__ void zero_words(uint32_t* p, int64_t n) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+// Device address of `scratch` on the current device `dev`, looked up on the
+// first call there (two threads racing store the same address).
+int scratch_address(int dev, uint8_t** out) {
+    ScratchSlot& s = g_scratch[dev];
+    uintptr_t p = s.ptr.load(std::memory_order_acquire);
+    if (p == 0) {
+        void* addr = nullptr;
+        if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr) return kLaunchError;
+        p = (uintptr_t)addr;
+        s.ptr.store(p, std::memory_order_release);
+    }
+    *out = reinterpret_cast<uint8_t*>(p);
+    return kOk;
+}
+
+}  // namespace
+}  // namespace iris
+
+extern "C" int iris_int4_paged_decode_attention_noalloc(
+    const void* query, const void* k_data, const void* v_data, const void* k_scale, const void* v_scale,
+    const int32_t* block_table, const int32_t* seq_lens, void* output, int32_t output_is_f32, int64_t batch,
+    int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size, int64_t num_pages,
+    int64_t max_pages, float softmax_scale, int32_t chunk_tiles, int32_t max_chunks, int32_t waves_per_block,
+    void* stream) {
+    using namespace iris;
+    if (batch <= 0) return kInvalidArgument;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) return kLaunchError;
+    uint8_t* ws = nullptr;
+    if (const int st = scratch_address(dev, &ws); st != kOk) return st;
+    ScratchSlot& slot = g_scratch[dev];
+    if (max_chunks > 1) {
+        // A split call needs its sequences' counters at zero.  Every call
+        // leaves the counters it used at zero, but a call with a smaller
+        // batch writes partials over the counters of the sequences past it.
+        const int64_t cb = counter_region_bytes(batch);
+        if (cb > kScratchBytes) return kWorkspaceTooSmall;
+        if (batch > slot.batch.load(std::memory_order_acquire)) {
+            const int64_t words = cb / 4;
+            const unsigned blocks = (unsigned)((words + 255) / 256 < 1024 ? (words + 255) / 256 : 1024);
+            hipLaunchKernelGGL(zero_words, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                               reinterpret_cast<uint32_t*>(ws), words);
+            if (hipGetLastError() != hipSuccess) return kLaunchError;
+        }
+    }
+    const int st = iris_int4_paged_decode_attention(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens,
+                                                    output, output_is_f32, ws, kScratchBytes, batch, num_q_heads,
+                                                    num_kv_heads, head_dim, page_size, num_pages, max_pages,
+                                                    softmax_scale, chunk_tiles, max_chunks, waves_per_block, stream);
+    if (st == kOk && max_chunks > 1) slot.batch.store(batch, std::memory_order_release);
+    return st;
+}
+
 extern "C" int iris_version(void) { return 100; }  // 0.1.0

@@ -36,6 +36,9 @@ _SIGNATURES = {
     "iris_int4_paged_decode_attention": [_p, _p, _p, _p, _p, _p, _p, _p, _i32, _p, _i64,
                                          _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                          ctypes.c_float, _i32, _i32, _i32, _p],
+    "iris_int4_paged_decode_attention_noalloc": [_p, _p, _p, _p, _p, _p, _p, _p, _i32, _i64,
+                                                 _i64, _i64, _i64, _i64, _i64, _i64,
+                                                 ctypes.c_float, _i32, _i32, _i32, _p],
     "iris_fp16_decode_plan": [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32,
                               ctypes.POINTER(_i32), ctypes.POINTER(_i32), ctypes.POINTER(_i64)],
     "iris_fp16_paged_decode_attention": [_p, _p, _p, _p, _p, _p, _i32, _p, _i64,

@@ -21,7 +21,8 @@ def declared_functions():
 
 def test_header_declares_the_entry_points():
     assert declared_functions() == sorted(["iris_rope_int4_paged_append", "iris_decode_plan",
-                                           "iris_int4_paged_decode_attention", "iris_version",
+                                           "iris_int4_paged_decode_attention",
+                                           "iris_int4_paged_decode_attention_noalloc", "iris_version",
                                            "iris_fp16_decode_plan", "iris_fp16_paged_decode_attention",
                                            "iris_rope_fp16_paged_append", "iris_quantize_pack_int4",
                                           "iris_decode_check", "iris_append_check"])
