@@ -311,35 +311,35 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(Args a)
 
     const int wg = xcd_remap(blockIdx.x, gridDim.x);
     const int b = wg / a.max_chunks, chunk = wg % a.max_chunks;
-    const int seq_len = a.seq_lens[b];
-    const int n_tiles = (seq_len + kTile - 1) / kTile;
     const int t_begin = chunk * a.chunk_tiles;
-    if (t_begin >= n_tiles) return;  // uniform over the workgroup
-    const int t_end = min(t_begin + a.chunk_tiles, n_tiles);
-    const int n_stages = t_end - t_begin;
-    const int n_chunks = (n_tiles + a.chunk_tiles - 1) / a.chunk_tiles;
     const int p0 = 2 * t_begin;
-    const int last_lp = (seq_len + kPage - 1) / kPage - 1;
+    const int seq_len = a.seq_lens[b];
 
     // ---- page ids of the chunk (logical page p0 + i in lane i of pid0 /
-    // pid1), then the raw query rows, both in flight together.
+    // pid1) and the raw query rows: neither depends on the sequence length,
+    // so they are in flight together with its load.
     const int32_t* bt = a.block_table + (int64_t)b * a.max_pages;
-    int pid0 = 0, pid1 = 0;
-    if (p0 + lane < a.max_pages) pid0 = bt[p0 + lane];
-    if (p0 + 64 + lane < a.max_pages) pid1 = bt[p0 + 64 + lane];
+    // (every lane loads, clamped into the table; no divergent branches
+    // around the loads, so none waits for another)
+    int pid0 = bt[min(p0 + lane, a.max_pages - 1)];
+    int pid1 = bt[min(p0 + 64 + lane, a.max_pages - 1)];
     // Query A operand: row n = (h, g) = (n >> 2, n & 3), nonzero only where
     // g == jq: 32 dims of group jq of head h.
     const half_t* qh = a.q + ((int64_t)b * a.n_q_heads + kvh * GQ) * D;
     u32x4_t qraw[4];
     {
-        const bool mine = (n & 3) == jq;
         const half_t* qrow = qh + (n >> 2) * D + 32 * jq;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            qraw[m] = u32x4_t{0, 0, 0, 0};
-            if (mine) qraw[m] = *reinterpret_cast<const u32x4_t*>(qrow + 8 * m);
-        }
+        for (int m = 0; m < 4; ++m) qraw[m] = *reinterpret_cast<const u32x4_t*>(qrow + 8 * m);
     }
+    asm volatile("" ::: "memory");  // keeps the loads above issued before the early return below
+
+    const int n_tiles = (seq_len + kTile - 1) / kTile;
+    if (t_begin >= n_tiles) return;  // uniform over the workgroup
+    const int t_end = min(t_begin + a.chunk_tiles, n_tiles);
+    const int n_stages = t_end - t_begin;
+    const int n_chunks = (n_tiles + a.chunk_tiles - 1) / a.chunk_tiles;
+    const int last_lp = (seq_len + kPage - 1) / kPage - 1;
 
     // ---- this wave's three loads of a slot (the same every step); each
     // fills 1 KiB of the slot, its lanes fetching the page chunks the
@@ -400,8 +400,11 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(Args a)
     for (int s = 0; s < kAhead; ++s) issue(s);
 
     half8_t qa[4];
+    {
+        const bool mine = (n & 3) == jq;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) qa[m] = q_operand(qraw[m]);
+        for (int m = 0; m < 4; ++m) qa[m] = q_operand(mine ? qraw[m] : u32x4_t{0, 0, 0, 0});
+    }
     // Accumulator start that removes the +8 of the K codes: C row (h, g)
     // gets -8 * 2^-24 * (sum of q over group g of head h, as the A operand
     // holds it, high-nibble dims / 16 counted 16 times).  Lane (4 h + g, g)
