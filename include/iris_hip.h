@@ -44,15 +44,20 @@ extern "C" {
  * made by `fused_rope_int4_paged_append` (src/iris_kernel/fused_kv.py:766-780;
  * kernel fused_kv.py:419-597), with the same contract: the result is
  * bit-identical to `torch_eager_append` (torch_eager_kv.py:110-337) for fp16
- * inputs with rotary_dim == head_dim and group_size == 32.
+ * inputs and group_size == 32.  K's first rotary_dim dims are rotated and
+ * the rest pass through, as in the eager path (torch_eager_kv.py:35-49); the
+ * reference's fused kernel only takes rotary_dim == head_dim
+ * (fused_kv.py:644-645), which its launch passes as head_dim.
  *
  *   key, value         [num_tokens, num_kv_heads, head_dim] fp16
  *   positions          [num_tokens] int32, row of cos/sin_cache per token
  *   slot_mapping       [num_tokens] int32, destination slot; < 0 = skip token
- *   cos_cache, sin_cache [max_position, head_dim / 2] fp16
+ *   cos_cache, sin_cache [max_position, rotary_dim / 2] fp16
  *   k_data .. v_scale  the cache, written in place at the valid slots only
  *
- * head_dim must be a multiple of 64 and at most 512.  Like the reference
+ * head_dim must be a multiple of 64 and at most 512; rotary_dim even, in
+ * [0, head_dim] (a multiple of 16 keeps the vector RoPE path; other values
+ * read each rotated dim's partner, cos and sin separately).  Like the reference
  * kernel, this function does not check slot or position ranges or duplicate
  * slots (fused_kv.py:741-759 does that on the host before launching).
  * num_pages and max_position are accepted for symmetry with the reference
@@ -62,8 +67,8 @@ int iris_rope_int4_paged_append(const void *key, const void *value, const int32_
                                 const int32_t *slot_mapping, const void *cos_cache,
                                 const void *sin_cache, void *k_data, void *v_data, void *k_scale,
                                 void *v_scale, int64_t num_tokens, int64_t num_kv_heads,
-                                int64_t head_dim, int64_t page_size, int64_t num_pages,
-                                int64_t max_position, void *stream);
+                                int64_t head_dim, int64_t rotary_dim, int64_t page_size,
+                                int64_t num_pages, int64_t max_position, void *stream);
 
 /*
  * RoPE(K) + paged append into an fp16 cache.  Replaces the TileLang launch

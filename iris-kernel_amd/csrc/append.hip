@@ -5,7 +5,10 @@
 // (src/iris_kernel/fused_kv.py:419-597 in Hunter2030ZeRo/Iris-Kernel) and
 // reproduces the eager semantics of `torch_eager_append`
 // (src/iris_kernel/torch_eager_kv.py:110-337) bit for bit for fp16 inputs
-// with rotary_dim == head_dim and group_size == 32.
+// and group_size == 32, with any even rotary_dim <= head_dim (the reference's
+// fused kernel requires rotary_dim == head_dim, fused_kv.py:644-645; its
+// eager path rotates the first rotary_dim dims and passes the rest through,
+// torch_eager_kv.py:35-49).
 //
 // Work mapping.  One (token, kv-head) row of D fp16 values is split into
 // D/8 chunks of 8 dims (16 bytes); lane c of a row owns dims [8c, 8c+8) of K
@@ -17,10 +20,14 @@
 // cache rows are adjacent in the NHD page layout, so the 32-bit code stores
 // of a wave cover whole cache lines.
 //
-// RoPE (rotate-half, as torch_eager_kv.py:38-47): dim i < D/2 pairs with
-// i + D/2, i.e. chunk c pairs with chunk c + D/16 (mod D/8).  Each product
-// and each sum is an fp16 operation, rounded to fp16 like torch's fp16 eager
-// ops; this file is built with -ffp-contract=off so no product is fused.
+// RoPE (rotate-half, as torch_eager_kv.py:38-47) on the first R = rotary_dim
+// dims: dim i < R/2 pairs with i + R/2.  When R is a multiple of 16 every
+// chunk lies in one rotary half or in the passthrough part, and chunk
+// c < R/8 pairs with chunk c +- R/16: one lane shuffle.  Other even R take
+// the per-element path (PER_ELEM): each rotated dim reads its partner, cos
+// and sin straight from memory.  Each product and each sum is an fp16
+// operation, rounded to fp16 like torch's fp16 eager ops; this file is built
+// with -ffp-contract=off so no product is fused.
 #include "common.h"
 #include "iris_hip.h"
 #include "quant.h"
@@ -31,24 +38,27 @@ namespace iris {
 // block's RPT * kRowsPerBlock, every load of all RPT rows issued before the
 // first use (the slot, position, K and V loads together, then the RoPE rows),
 // so a wave keeps RPT rows of loads in flight.  Large appends use RPT = 2.
-template <int ROWLANES, int RPT>
+template <int ROWLANES, int RPT, bool PER_ELEM>
 __global__ __launch_bounds__(256) void rope_int4_paged_append_kernel(
     const u32x4_t* __restrict__ key, const u32x4_t* __restrict__ value,
     const int32_t* __restrict__ positions, const int32_t* __restrict__ slot_mapping,
     const half_t* __restrict__ cos_cache, const half_t* __restrict__ sin_cache,
     uint32_t* __restrict__ k_data, uint32_t* __restrict__ v_data,
     half_t* __restrict__ k_scale, half_t* __restrict__ v_scale,
-    int64_t n_rows, int n_heads, int head_dim, int page_size) {
+    int64_t n_rows, int n_heads, int head_dim, int rotary_dim, int page_size) {
     constexpr int kRowsPerBlock = 256 / ROWLANES;
     const int chunks = head_dim >> 3;  // 8 dims per lane
     const int lane = threadIdx.x & 63;
     const int c_raw = threadIdx.x & (ROWLANES - 1);
     const int c = c_raw < chunks ? c_raw : 0;  // padding lanes mirror chunk 0
-    const int half_chunks = chunks >> 1;
-    const int cc = c < half_chunks ? c : c - half_chunks;
-    const bool lo_half = c < half_chunks;
-    // RoPE partner chunk from the lane half a row away.
-    const int partner = (lane - c_raw) + (c < half_chunks ? c + half_chunks : c - half_chunks);
+    const int hr = rotary_dim >> 1;            // RoPE table width
+    // Chunk-aligned RoPE (R % 16 == 0): chunks below R/8 rotate with the
+    // chunk R/16 away; cos/sin chunk cc of the table row.
+    const int rot_c = rotary_dim >> 3, half_c = rotary_dim >> 4;
+    const bool rotated = !PER_ELEM && c < rot_c;
+    const bool lo_half = c < half_c;
+    const int cc = lo_half ? c : c - half_c;
+    const int partner = (lane - c_raw) + (lo_half ? c + half_c : (rotated ? c - half_c : c));
 
     int64_t rr[RPT];
     bool live[RPT];
@@ -69,11 +79,14 @@ __global__ __launch_bounds__(256) void rope_int4_paged_append_kernel(
     u32x4_t cx[RPT], sx[RPT];
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
+        cx[k] = sx[k] = u32x4_t{0, 0, 0, 0};
         // Positions of skipped tokens are not validated by the caller; read
         // the RoPE table at row 0 for them (the result is discarded).
         const int64_t p = slot[k] >= 0 ? pos[k] : 0;
-        cx[k] = *reinterpret_cast<const u32x4_t*>(cos_cache + p * (head_dim >> 1) + cc * 8);
-        sx[k] = *reinterpret_cast<const u32x4_t*>(sin_cache + p * (head_dim >> 1) + cc * 8);
+        if (rotated) {
+            cx[k] = *reinterpret_cast<const u32x4_t*>(cos_cache + p * hr + cc * 8);
+            sx[k] = *reinterpret_cast<const u32x4_t*>(sin_cache + p * hr + cc * 8);
+        }
     }
 
 #pragma unroll
@@ -90,8 +103,31 @@ __global__ __launch_bounds__(256) void rope_int4_paged_append_kernel(
             half2_t oth = as_half2(kp[q]);
             half2_t a = own * as_half2(cx[k][q]);  // x*cos, rounded to fp16
             half2_t b = oth * as_half2(sx[k][q]);  // x'*sin, rounded to fp16
-            kr[q] = lo_half ? a - b : a + b;       // rounded to fp16
+            kr[q] = rotated ? (lo_half ? a - b : a + b) : own;  // rounded to fp16
             vr[q] = as_half2(vx[k][q]);
+        }
+        if constexpr (PER_ELEM) {
+            // Any even R: dim d < R takes its partner, cos and sin from memory.
+            const half_t* krow = reinterpret_cast<const half_t*>(key) + rr[k] * head_dim;
+            const int64_t p = slot[k] >= 0 ? pos[k] : 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int d = 8 * c + j;
+                if (d < rotary_dim) {
+                    const bool lo = d < hr;
+                    const int ci = lo ? d : d - hr;
+                    const half_t x = j & 1 ? kr[j >> 1].y : kr[j >> 1].x;
+                    const half_t xp = krow[lo ? d + hr : d - hr];
+                    const half_t ea = x * cos_cache[p * hr + ci];   // rounded to fp16
+                    const half_t eb = xp * sin_cache[p * hr + ci];  // rounded to fp16
+                    const half_t y = lo ? ea - eb : ea + eb;
+                    if (j & 1) kr[j >> 1].y = y;
+                    else kr[j >> 1].x = y;
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
             kmax2 = amax_max(kmax2, __builtin_elementwise_abs(kr[q]));
             vmax2 = amax_max(vmax2, __builtin_elementwise_abs(vr[q]));
         }
@@ -129,12 +165,12 @@ using namespace iris;
 extern "C" int iris_rope_int4_paged_append(
     const void* key, const void* value, const int32_t* positions, const int32_t* slot_mapping,
     const void* cos_cache, const void* sin_cache, void* k_data, void* v_data, void* k_scale,
-    void* v_scale, int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
-    int64_t num_pages, int64_t max_position, void* stream) {
+    void* v_scale, int64_t num_tokens, int64_t num_kv_heads, int64_t head_dim, int64_t rotary_dim,
+    int64_t page_size, int64_t num_pages, int64_t max_position, void* stream) {
     (void)num_pages;
     (void)max_position;
     if (num_tokens < 0 || num_kv_heads <= 0 || page_size <= 0 || head_dim <= 0 ||
-        head_dim % 64 != 0 || head_dim > 512)
+        head_dim % 64 != 0 || head_dim > 512 || rotary_dim < 0 || rotary_dim > head_dim || rotary_dim % 2 != 0)
         return kInvalidArgument;
     if (num_tokens == 0) return kOk;
     const int64_t n_rows = num_tokens * num_kv_heads;
@@ -149,14 +185,17 @@ extern "C" int iris_rope_int4_paged_append(
     const int64_t blocks = (n_rows + rows_per_block * rpt - 1) / (rows_per_block * rpt);
     if (blocks > 0x7FFFFFFF) return kInvalidArgument;
     hipStream_t s = (hipStream_t)stream;
-#define IRIS_LAUNCH_APPEND(RL, RPT)                                                                  \
-    hipLaunchKernelGGL((rope_int4_paged_append_kernel<RL, RPT>), dim3((unsigned)blocks), dim3(256), 0, s, \
-                       (const u32x4_t*)key, (const u32x4_t*)value, positions, slot_mapping,          \
-                       (const half_t*)cos_cache, (const half_t*)sin_cache, (uint32_t*)k_data,        \
-                       (uint32_t*)v_data, (half_t*)k_scale, (half_t*)v_scale, n_rows,                \
-                       (int)num_kv_heads, (int)head_dim, (int)page_size)
-#define IRIS_LAUNCH_APPEND_RPT(RL) \
-    if (rpt == 2) IRIS_LAUNCH_APPEND(RL, 2); else IRIS_LAUNCH_APPEND(RL, 1)
+    const bool per_elem = rotary_dim % 16 != 0;
+#define IRIS_LAUNCH_APPEND(RL, RPT, PE)                                                                  \
+    hipLaunchKernelGGL((rope_int4_paged_append_kernel<RL, RPT, PE>), dim3((unsigned)blocks), dim3(256), 0, s, \
+                       (const u32x4_t*)key, (const u32x4_t*)value, positions, slot_mapping,              \
+                       (const half_t*)cos_cache, (const half_t*)sin_cache, (uint32_t*)k_data,            \
+                       (uint32_t*)v_data, (half_t*)k_scale, (half_t*)v_scale, n_rows,                    \
+                       (int)num_kv_heads, (int)head_dim, (int)rotary_dim, (int)page_size)
+#define IRIS_LAUNCH_APPEND_RPT(RL)                   \
+    if (per_elem) IRIS_LAUNCH_APPEND(RL, 1, true);   \
+    else if (rpt == 2) IRIS_LAUNCH_APPEND(RL, 2, false); \
+    else IRIS_LAUNCH_APPEND(RL, 1, false)
     switch (rowlanes) {
         case 8: IRIS_LAUNCH_APPEND_RPT(8); break;
         case 16: IRIS_LAUNCH_APPEND_RPT(16); break;

@@ -29,7 +29,7 @@ _i32 = ctypes.c_int32
 
 _SIGNATURES = {
     "iris_rope_int4_paged_append": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
-                                    _i64, _i64, _i64, _i64, _i64, _i64, _p],
+                                    _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p],
     "iris_decode_plan": [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32,
                          ctypes.POINTER(_i32), ctypes.POINTER(_i32), ctypes.POINTER(_i32),
                          ctypes.POINTER(_i64)],

@@ -48,7 +48,7 @@ def _require_dense(name: str, t: torch.Tensor, align: int) -> None:
 
 
 def _launch_append(key, value, positions, slot_mapping, cos_cache, sin_cache, k_data, v_data,
-                   k_scale, v_scale, head_dim: int, page_size: int) -> None:
+                   k_scale, v_scale, head_dim: int, rotary_dim: int, page_size: int) -> None:
     if key.shape[0] == 0 or cos_cache.shape[0] == 0:
         return  # nothing to write (an empty RoPE table admits no valid token)
     key = _dense(key, 16)
@@ -65,8 +65,8 @@ def _launch_append(key, value, positions, slot_mapping, cos_cache, sin_cache, k_
     status = _lib.lib().iris_rope_int4_paged_append(
         key.data_ptr(), value.data_ptr(), positions.data_ptr(), slot_mapping.data_ptr(),
         cos_cache.data_ptr(), sin_cache.data_ptr(), k_data.data_ptr(), v_data.data_ptr(),
-        k_scale.data_ptr(), v_scale.data_ptr(), key.shape[0], key.shape[1], head_dim, page_size,
-        k_data.shape[0], cos_cache.shape[0], stream)
+        k_scale.data_ptr(), v_scale.data_ptr(), key.shape[0], key.shape[1], head_dim, rotary_dim,
+        page_size, k_data.shape[0], cos_cache.shape[0], stream)
     _lib.check(status, "iris_rope_int4_paged_append")
 
 
@@ -89,7 +89,10 @@ def fused_rope_int4_paged_append(
     """RoPE(K), quantise K and V to group-32 INT4, pack, scatter into the pages.
 
     Bit-identical to ``torch_eager_append`` for the scope it accepts
-    (fp16, head_dim % 64 == 0, rotary_dim == head_dim, group_size == 32).
+    (fp16, head_dim % 64 == 0, group_size == 32, any even rotary_dim <=
+    head_dim: the first rotary_dim dims of K are rotated, the rest pass
+    through, as the eager path does; the reference's fused kernel requires
+    rotary_dim == head_dim).
     Slots < 0 are skipped.  Mutates k_data/v_data/k_scale/v_scale in place;
     the launch is asynchronous on the current stream.
     """
@@ -111,8 +114,12 @@ def fused_rope_int4_paged_append(
         raise NotImplementedError("Stage C currently requires head_dim divisible by 64")
     if group_size != 32:
         raise NotImplementedError("Stage C currently supports group_size=32")
-    if rotary_dim != head_dim:
-        raise NotImplementedError("Stage C currently requires rotary_dim == head_dim")
+    # Partial RoPE is accepted (the eager path's rule, torch_eager_kv.py:35-49,
+    # where the reference's fused path raises NotImplementedError).
+    if rotary_dim < 0:
+        raise ValueError("rotary_dim must be non-negative")
+    if rotary_dim > head_dim:
+        raise ValueError("rotary_dim cannot exceed head_dim")
     if rotary_dim % 2 != 0:
         raise ValueError("rotary_dim must be even")
     if page_size <= 0:
@@ -187,7 +194,7 @@ def fused_rope_int4_paged_append(
     if not any_valid:
         return  # the kernel would skip every token
     _launch_append(key, value, positions, slot_mapping, cos_cache, sin_cache, k_data, v_data,
-                   k_scale, v_scale, head_dim, page_size)
+                   k_scale, v_scale, head_dim, rotary_dim, page_size)
 
 
 def _rope_int4_paged_append(key, value, positions, slot_mapping, cos_cache, sin_cache, k_data,
@@ -199,7 +206,7 @@ def _rope_int4_paged_append(key, value, positions, slot_mapping, cos_cache, sin_
     ignored (the HIP launch shape is fixed by the kernel)."""
     del threads
     _launch_append(key, value, positions, slot_mapping, cos_cache, sin_cache, k_data, v_data,
-                   k_scale, v_scale, head_dim, page_size)
+                   k_scale, v_scale, head_dim, head_dim, page_size)
 
 
 # ------------------------------------------------------- FP16 cache append

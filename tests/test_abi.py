@@ -41,11 +41,15 @@ def test_append_rejects_unsupported_head_dim_before_launch():
     null = None
     for d in (96, 0, 576):
         st = lib.iris_rope_int4_paged_append(null, null, null, null, null, null, null, null, null,
-                                             null, 4, 2, d, 16, 8, 16, null)
+                                             null, 4, 2, d, d, 16, 8, 16, null)
+        assert st == 1
+    for rot in (-2, 130, 63):  # negative, past head_dim, odd
+        st = lib.iris_rope_int4_paged_append(null, null, null, null, null, null, null, null, null,
+                                             null, 4, 2, 128, rot, 16, 8, 16, null)
         assert st == 1
     # zero tokens is a no-op that touches nothing
     assert lib.iris_rope_int4_paged_append(null, null, null, null, null, null, null, null, null,
-                                           null, 0, 2, 128, 16, 8, 16, null) == 0
+                                           null, 0, 2, 128, 64, 16, 8, 16, null) == 0
 
 
 def test_decode_rejects_unsupported_shapes_before_launch():

@@ -183,7 +183,10 @@ def _small(device):
     (lambda a, kw: a.update(key=a["key"].float(), value=a["value"].float()), TypeError),
     (lambda a, kw: a.update(cos_cache=a["cos_cache"].float()), TypeError),
     (lambda a, kw: kw.update(group_size=16), NotImplementedError),
-    (lambda a, kw: kw.update(rotary_dim=32), NotImplementedError),
+    (lambda a, kw: kw.update(rotary_dim=32), ValueError),   # cos/sin width 32 is not rotary_dim // 2
+    (lambda a, kw: kw.update(rotary_dim=66), ValueError),
+    (lambda a, kw: kw.update(rotary_dim=-2), ValueError),
+    (lambda a, kw: kw.update(rotary_dim=63), ValueError),
     (lambda a, kw: a.update(k_data=a["k_data"][:, :8]), ValueError),
     (lambda a, kw: a.update(key=a["key"].cpu()), ValueError),
 ])
@@ -193,6 +196,31 @@ def test_validation_errors(device, mutate, exc):
     mutate(a, kw)
     with pytest.raises(exc):
         fused_rope_int4_paged_append(**a, **kw)
+
+
+@pytest.mark.parametrize("head_dim,rotary_dim", [
+    (128, 0), (128, 16), (128, 64), (128, 96), (128, 112),   # multiples of 16: vector RoPE path
+    (128, 2), (128, 6), (128, 34), (128, 100), (128, 126),   # per-element path
+    (64, 32), (64, 10), (256, 128), (256, 250), (512, 256)])
+def test_partial_rotary_bit_exact(device, head_dim, rotary_dim):
+    # Partial RoPE as the eager path defines it (torch_eager_kv.py:35-49):
+    # the first rotary_dim dims rotate, the rest pass through.
+    log(f"append: partial rotary D={head_dim} R={rotary_dim}")
+    g = torch.Generator().manual_seed(head_dim * 1000 + rotary_dim)
+    T, H, NP, P = 37, 3, 6, 16
+    key = (torch.randn(T, H, head_dim, generator=g) * 3).to(torch.float16)
+    value = (torch.randn(T, H, head_dim, generator=g) * 3).to(torch.float16)
+    pos = torch.randint(0, 500, (T,), generator=g, dtype=torch.int32)
+    slots = torch.randperm(NP * P, generator=g)[:T].to(torch.int32)
+    slots[::7] = -1
+    ang = torch.rand(500, rotary_dim // 2, generator=g) * 300
+    cos, sin = ang.cos().to(torch.float16), ang.sin().to(torch.float16)
+    cache = (torch.randint(0, 256, (NP, P, H, head_dim // 2), dtype=torch.uint8, generator=g),
+             torch.randint(0, 256, (NP, P, H, head_dim // 2), dtype=torch.uint8, generator=g),
+             torch.randn(NP, P, H, head_dim // 32, generator=g).to(torch.float16),
+             torch.randn(NP, P, H, head_dim // 32, generator=g).to(torch.float16))
+    ref, gpu = run_both(device, key, value, pos, slots, cos, sin, cache, rotary_dim)
+    assert_same(ref, gpu)
 
 
 def test_invalid_slot_positions_are_not_read(device):
