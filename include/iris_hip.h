@@ -121,6 +121,8 @@ int iris_quantize_pack_int4(const void *x, void *packed, void *scales, int64_t n
  * total_tokens and max_tokens (sum and max of seq_lens) may be -1 if
  * unknown; max_pages (columns of block_table) bounds them.
  * tokens_per_split > 0 and waves_per_block > 0 override the heuristic.
+ * max_pages counts 16-token pages: block_table columns * page_size / 16.
+ * head_dim 64, 128 or 256; any num_q_heads / num_kv_heads.
  */
 int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                      int64_t max_pages, int64_t total_tokens, int64_t max_tokens,
@@ -165,8 +167,12 @@ int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, i
  *                max_chunks; past that the launch writes NaN into every
  *                output element rather than a wrong result)
  *
- * page_size must be 16, head_dim 64 or 128, num_q_heads / num_kv_heads at
- * most 16 (fused_attention.py:390-403).  Page ids and lengths are not
+ * page_size 16 << k (16 to 256), head_dim 64, 128 or 256, and any
+ * num_q_heads / num_kv_heads (the reference's fused path takes page_size 16,
+ * head_dim 64 or 128 and at most 16 query heads per kv head,
+ * fused_attention.py:390-403; its eager path takes any).  max_pages is the
+ * number of block_table columns; plan with max_pages * page_size / 16.
+ * Page ids and lengths are not
  * range-checked on the device (fused_attention.py:415-429 does that on the
  * host).  Tokens of the last page beyond seq_lens[b] are read but never
  * contribute, even if their scales are NaN.

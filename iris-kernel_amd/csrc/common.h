@@ -69,6 +69,15 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expect) 
     return last;
 }
 
+// Pages of page_size = 16 << page_shift tokens are read as 1 << page_shift
+// consecutive 16-token pages (the [num_pages, page_size, ...] cache is the
+// same bytes as a [num_pages << page_shift, 16, ...] one): virtual 16-token
+// page vp of a block-table row is 16-token page
+// (row[vp >> page_shift] << page_shift) + (vp & ((1 << page_shift) - 1)).
+__device__ __forceinline__ int virtual_page(const int32_t* row, int vp, int page_shift) {
+    return (row[vp >> page_shift] << page_shift) | (vp & ((1 << page_shift) - 1));
+}
+
 // LDS a workgroup may use on gfx950 (per CU).
 constexpr int kMaxLdsBytes = 160 * 1024;
 

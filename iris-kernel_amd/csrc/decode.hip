@@ -95,8 +95,11 @@ struct DecodeArgs {
     float* ws_ml;        // [B][max_chunks][n_kv_blocks][16][2]   (m, l), base-2 logits
     int out_f32;
     int batch, n_q_heads, n_kv_heads, group;  // group = Hq / Hkv
-    int max_pages;
-    int n_kv_blocks, max_chunks, chunk_tiles;
+    int max_pages;            // 16-token pages a block-table row addresses
+    int bt_cols, page_shift;  // block-table columns; page_size = 16 << page_shift
+    // kv blocks: (KVW kv heads) x (q_blocks blocks of 16 of a kv head's
+    // query heads; q_blocks > 1 only for group > 16, with KVW = 1)
+    int n_kv_blocks, q_blocks, max_chunks, chunk_tiles;
     float log2_scale;  // softmax_scale * log2(e)
 };
 
@@ -294,7 +297,7 @@ struct DecodeLayout {
 };
 
 template <int D, int KVW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void int4_decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void int4_decode_kernel(DecodeArgs a) {
     using L = DecodeLayout<D, KVW>;
     constexpr int G = L::G, HB = L::HB, C = L::C, SSEG = L::SSEG;
     static_assert(C >= 2 && (C & (C - 1)) == 0, "chunks per token must be a power of two >= 2");
@@ -311,23 +314,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void i
     const int rest = wg / a.n_kv_blocks;
     const int chunk = rest % a.max_chunks;
     const int b = rest / a.max_chunks;
-    const int kv0 = kvb * KVW;
+    const int kv0 = (kvb / a.q_blocks) * KVW;
     const int g = a.group;
+    const int qoff = (kvb % a.q_blocks) * 16;  // first query head of the block (within the kv head)
     const int hkv = a.n_kv_heads;
     const int t_begin = chunk * a.chunk_tiles;
     const int p0 = 2 * t_begin;  // first logical page of the chunk
 
     // ---- loads that depend on nothing else go first: the chunk's page ids
     // (lane i holds logical pages p0 + i and p0 + 64 + i) and q.
-    const int32_t* bt = a.block_table + (int64_t)b * a.max_pages;
+    const int32_t* bt = a.block_table + (int64_t)b * a.bt_cols;
     int pid0 = 0, pid1 = 0;
-    if (p0 + lane < a.max_pages) pid0 = bt[p0 + lane];
-    if (p0 + 64 + lane < a.max_pages) pid1 = bt[p0 + 64 + lane];
+    if (p0 + lane < a.max_pages) pid0 = virtual_page(bt, p0 + lane, a.page_shift);
+    if (p0 + 64 + lane < a.max_pages) pid1 = virtual_page(bt, p0 + 64 + lane, a.page_shift);
 
-    // Column n of the MFMA tiles = (kv head kv0 + n / g, query head n % g).
-    const bool col_valid = n < KVW * g;
-    const int col_kv = col_valid ? n / g : 0;
-    const int hq = kv0 * g + n;
+    // Column n of the MFMA tiles = (kv head kv0 + n / g, query head n % g),
+    // or, for g > 16, query head qoff + n of kv head kv0.
+    const int n_cols = a.q_blocks > 1 ? min(16, g - qoff) : KVW * g;
+    const bool col_valid = n < n_cols;
+    const int col_kv = col_valid && a.q_blocks == 1 ? n / g : 0;
+    const int hq = kv0 * g + qoff + n;
     u32x4_t qraw[G];
 #pragma unroll
     for (int grp = 0; grp < G; ++grp) {
@@ -724,7 +730,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void i
     __syncthreads();
     // Every thread serves one column (threadIdx % 16) for all its elements.
     const int col = threadIdx.x & 15;
-    const int n_cols = KVW * g;
     float fw[4];
     float mstar = -INFINITY;
 #pragma unroll
@@ -749,7 +754,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void i
         return acc * inv_l;
     };
     auto store_out = [&](int idx, float val) {
-        const int64_t oi = ((int64_t)b * a.n_q_heads + kv0 * g + col) * D + c_order_dim(idx);
+        const int64_t oi = ((int64_t)b * a.n_q_heads + kv0 * g + qoff + col) * D + c_order_dim(idx);
         if (a.out_f32) reinterpret_cast<float*>(a.out)[oi] = val;
         else reinterpret_cast<half_t*>(a.out)[oi] = (half_t)val;
     };
@@ -798,8 +803,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void i
     // so up to CB chunks cost one memory round trip.
     // (8 at D = 64: the batch's registers set the kernel's VGPR count, and
     // there the tile loop needs fewer, so a smaller batch keeps more waves
-    // resident; MI355X, configuration 4: 30.7 -> 29.4 us.)
-    constexpr int CB = D == 64 ? 8 : 16;
+    // resident; MI355X, configuration 4: 30.7 -> 29.4 us.  8 at D = 256,
+    // whose tile loop holds twice the accumulators.)
+    constexpr int CB = D == 128 ? 16 : 8;
     for (int base = threadIdx.x; base < 16 * D; base += 8 * (int)blockDim.x) {
         float acc[8];
 #pragma unroll
@@ -842,14 +848,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void i
     }
 }
 
+// Blocks of 16 query heads per kv head (more than one only for Hq / Hkv > 16,
+// each a workgroup of its own over the same pages).
+static int query_blocks(int g) { return g > 16 ? (g + 15) / 16 : 1; }
+
 // kv heads per wavefront: as many as fit in 16 MFMA columns (at most 4),
 // dividing Hkv -- and fewer while the grid would hold under 512 wave-tiles
 // at the block table's capacity (B=1-sized calls), which spreads the tile
 // work over more waves (MI355X, B=1, Hq=32, Hkv=8, D=128: L=128
 // 8.5 -> 6.9 us, L=512 12.4 -> 10.3 us, L=4096 15.2 -> 14.5 us).  Plan and
 // launch see the same four values, so they agree.
-static int pick_kvw(int g, int hkv, int64_t batch, int64_t max_pages) {
-    int kvw = 4;
+static int pick_kvw(int g, int hkv, int64_t batch, int64_t max_pages, int64_t head_dim) {
+    int kvw = head_dim == 256 ? 1 : 4;
     while (kvw > 1 && (kvw * g > 16 || hkv % kvw != 0)) kvw >>= 1;
     const int64_t cap_tiles = (max_pages * kPageSize + kTile - 1) / kTile;
     while (kvw > 1 && batch * (cap_tiles + 1) * (hkv / kvw) < 512) kvw >>= 1;
@@ -927,7 +937,7 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
                                 int32_t* out_max_chunks, int32_t* out_waves,
                                 int64_t* out_workspace_bytes) {
     if (batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
-        num_q_heads / num_kv_heads > 16 || (head_dim != 64 && head_dim != 128) || max_pages <= 0)
+        (head_dim != 64 && head_dim != 128 && head_dim != 256) || max_pages <= 0 || max_pages > 0x3FFFFFFF)
         return kInvalidArgument;
     // Unknown lengths (the sync-free positional handle): the widest batch
     // block_table admits stands in for them.
@@ -940,8 +950,8 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
         return pages_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, total_tokens, max_tokens,
                           tokens_per_split, out_chunk_tiles, out_max_chunks, out_waves, out_workspace_bytes);
     const int g = (int)(num_q_heads / num_kv_heads);
-    const int kvw = pick_kvw(g, (int)num_kv_heads, batch, max_pages);
-    const int64_t n_kvb = num_kv_heads / kvw;
+    const int kvw = pick_kvw(g, (int)num_kv_heads, batch, max_pages, head_dim);
+    const int64_t n_kvb = num_kv_heads / kvw * query_blocks(g);
     const int64_t cap_tokens = max_pages * kPageSize;
     if (max_tokens < 0 || max_tokens > cap_tokens) max_tokens = cap_tokens;
     if (total_tokens < 0) total_tokens = batch * max_tokens;
@@ -975,7 +985,7 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
     // chunks than one merge batch reads at once (MI355X: configuration 1
     // 7.4 -> 6.2 us; B=1, Hq=32, Hkv=8, D=128, L=4096: 14.6 -> 12.9 us).
     if (tokens_per_split <= 0 && batch * n_kvb * max_chunks <= 256) {
-        const int64_t merge_batch = head_dim == 64 ? 8 : 16;  // CB of the kernel's merge
+        const int64_t merge_batch = head_dim == 128 ? 16 : 8;  // CB of the kernel's merge
         if (2 * chunk_tiles >= longest_tiles && max_tiles <= kMaxChunkTiles) {
             chunk_tiles = max_tiles;
         } else {
@@ -1002,21 +1012,27 @@ extern "C" int iris_int4_paged_decode_attention(
     int64_t num_pages, int64_t max_pages, float softmax_scale, int32_t chunk_tiles,
     int32_t max_chunks, int32_t waves_per_block, void* stream) {
     (void)num_pages;
-    if (page_size != kPageSize || batch <= 0 || num_kv_heads <= 0 ||
-        num_q_heads % num_kv_heads != 0 || num_q_heads / num_kv_heads > 16 ||
-        (head_dim != 64 && head_dim != 128) || max_pages <= 0)
+    // page_size = 16 << shift: each table entry stands for 1 << shift
+    // consecutive 16-token pages, so the kernels see max_pages << shift of
+    // them per row (the count the plan was made with).
+    int shift = 0;
+    while (shift < 5 && (kPageSize << shift) != page_size) ++shift;
+    if (shift == 5 || batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
+        (head_dim != 64 && head_dim != 128 && head_dim != 256) || max_pages <= 0 || (max_pages << shift) > 0x3FFFFFFF)
         return kInvalidArgument;
+    const int64_t bt_cols = max_pages;
+    max_pages <<= shift;
     if (waves_per_block == pages_waves() && pages_allowed(waves_per_block) &&
         pages_supported(num_q_heads, num_kv_heads, head_dim, max_pages))
         return pages_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
                             workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, max_pages,
-                            softmax_scale, chunk_tiles, max_chunks, stream);
+                            bt_cols, shift, softmax_scale, chunk_tiles, max_chunks, stream);
     if (chunk_tiles <= 0 || chunk_tiles > kMaxChunkTiles || max_chunks <= 0 || waves_per_block <= 0 ||
         waves_per_block > 4)
         return kInvalidArgument;
     if ((int64_t)chunk_tiles * max_chunks * 2 < max_pages) return kInvalidArgument;
     const int g = (int)(num_q_heads / num_kv_heads);
-    const int kvw = pick_kvw(g, (int)num_kv_heads, batch, max_pages);
+    const int kvw = pick_kvw(g, (int)num_kv_heads, batch, max_pages, head_dim);
     DecodeArgs a;
     a.q = (const half_t*)query;
     a.k_data = (const uint8_t*)k_data;
@@ -1032,7 +1048,11 @@ extern "C" int iris_int4_paged_decode_attention(
     a.n_kv_heads = (int)num_kv_heads;
     a.group = g;
     a.max_pages = (int)max_pages;
-    a.n_kv_blocks = (int)(num_kv_heads / kvw);
+    a.bt_cols = (int)bt_cols;
+    a.page_shift = shift;
+    a.q_blocks = query_blocks(g);
+    if ((int64_t)(num_kv_heads / kvw) * a.q_blocks > 0x7FFFFFFF) return kInvalidArgument;
+    a.n_kv_blocks = (int)(num_kv_heads / kvw) * a.q_blocks;
     a.max_chunks = max_chunks;
     a.chunk_tiles = chunk_tiles;
     a.log2_scale = softmax_scale * 1.4426950408889634f;
@@ -1056,6 +1076,8 @@ extern "C" int iris_int4_paged_decode_attention(
         if (kvw == 4) st = launch_decode<128, 4>(grid, block, waves_per_block, s, a);
         else if (kvw == 2) st = launch_decode<128, 2>(grid, block, waves_per_block, s, a);
         else st = launch_decode<128, 1>(grid, block, waves_per_block, s, a);
+    } else if (head_dim == 256) {
+        st = launch_decode<256, 1>(grid, block, waves_per_block, s, a);
     } else {
         if (kvw == 4) st = launch_decode<64, 4>(grid, block, waves_per_block, s, a);
         else if (kvw == 2) st = launch_decode<64, 2>(grid, block, waves_per_block, s, a);

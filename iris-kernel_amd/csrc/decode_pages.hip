@@ -112,7 +112,8 @@ struct Args {
     float* p2_ml;        // [slots][Hq][2]
     int out_f32;
     int batch, n_q_heads, n_kv_heads, group;  // group = Hq / Hkv
-    int max_pages;
+    int max_pages;                // 16-token pages a block-table row addresses
+    int bt_cols, page_shift;      // block-table columns; page_size = 16 << page_shift
     int max_chunks, chunk_tiles;  // chunk mode: workgroup (b, chunk), b * max_chunks + chunk
     int segmented;                // balanced mode: workgroup w takes tiles [w T / W, (w + 1) T / W)
     int slots;                    // workgroups + B
@@ -383,10 +384,10 @@ __global__ __launch_bounds__(64 * kMaxWaves) void int4_decode_pages_kernel(Args 
                        const int first) __attribute__((always_inline)) {
     const int p0 = 2 * t_begin;
 
-    const int32_t* bt = a.block_table + (int64_t)b * a.max_pages;
+    const int32_t* bt = a.block_table + (int64_t)b * a.bt_cols;
     int pid0 = 0, pid1 = 0;
-    if (p0 + lane < a.max_pages) pid0 = bt[p0 + lane];
-    if (p0 + 64 + lane < a.max_pages) pid1 = bt[p0 + 64 + lane];
+    if (p0 + lane < a.max_pages) pid0 = virtual_page(bt, p0 + lane, a.page_shift);
+    if (p0 + 64 + lane < a.max_pages) pid1 = virtual_page(bt, p0 + 64 + lane, a.page_shift);
 
     // Column n = (query head h, scale slot gs); this lane's K quarter row
     // lies in group gl = jq * G / 4.  Pass p puts group p * GS + gs in the
@@ -1162,8 +1163,8 @@ int64_t pages_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_d
 int pages_launch(const void* query, const void* k_data, const void* v_data, const void* k_scale, const void* v_scale,
                  const int32_t* block_table, const int32_t* seq_lens, void* output, int32_t output_is_f32,
                  void* workspace, int64_t workspace_bytes_avail, int64_t batch, int64_t num_q_heads,
-                 int64_t num_kv_heads, int64_t head_dim, int64_t max_pages, float softmax_scale, int32_t chunk_tiles,
-                 int32_t max_chunks, void* stream) {
+                 int64_t num_kv_heads, int64_t head_dim, int64_t max_pages, int64_t bt_cols, int32_t page_shift,
+                 float softmax_scale, int32_t chunk_tiles, int32_t max_chunks, void* stream) {
     const int hkv = (int)num_kv_heads;
     // chunk_tiles > 0: chunk mode, batch x max_chunks workgroups of
     // chunk_tiles tiles; < 0: the balanced mode, max_chunks workgroups
@@ -1178,7 +1179,7 @@ int pages_launch(const void* query, const void* k_data, const void* v_data, cons
         stream_allowed())
         return stream_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
                              workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, max_pages,
-                             softmax_scale, chunk_tiles, max_chunks, stream);
+                             bt_cols, page_shift, softmax_scale, chunk_tiles, max_chunks, stream);
     if (!balanced && share * max_chunks * 2 < max_pages) return kInvalidArgument;
     if (balanced && max_chunks > 8 * pg::kMaxGroups) return kInvalidArgument;
     const int g = (int)(num_q_heads / num_kv_heads);
@@ -1205,6 +1206,8 @@ int pages_launch(const void* query, const void* k_data, const void* v_data, cons
     a.n_kv_heads = hkv;
     a.group = g;
     a.max_pages = (int)max_pages;
+    a.bt_cols = (int)bt_cols;
+    a.page_shift = page_shift;
     a.max_chunks = max_chunks;
     a.chunk_tiles = (int)share;
     a.segmented = balanced ? 1 : 0;

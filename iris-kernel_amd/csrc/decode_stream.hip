@@ -114,7 +114,9 @@ struct Args {
     float* part_o;       // [B][max_chunks][Hq][D] o / l of each chunk
     float* part_ml;      // [B][max_chunks][Hq][2] (m, l), base-2 logits
     int out_f32;
-    int batch, n_q_heads, max_pages, max_chunks, chunk_tiles;
+    int batch, n_q_heads, max_chunks, chunk_tiles;
+    int max_pages;            // 16-token pages a block-table row addresses
+    int bt_cols, page_shift;  // block-table columns; page_size = 16 << page_shift
     float log2_scale;
 };
 
@@ -318,11 +320,11 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(Args a)
     // ---- page ids of the chunk (logical page p0 + i in lane i of pid0 /
     // pid1) and the raw query rows: neither depends on the sequence length,
     // so they are in flight together with its load.
-    const int32_t* bt = a.block_table + (int64_t)b * a.max_pages;
+    const int32_t* bt = a.block_table + (int64_t)b * a.bt_cols;
     // (every lane loads, clamped into the table; no divergent branches
     // around the loads, so none waits for another)
-    int pid0 = bt[min(p0 + lane, a.max_pages - 1)];
-    int pid1 = bt[min(p0 + 64 + lane, a.max_pages - 1)];
+    int pid0 = virtual_page(bt, min(p0 + lane, a.max_pages - 1), a.page_shift);
+    int pid1 = virtual_page(bt, min(p0 + 64 + lane, a.max_pages - 1), a.page_shift);
     // Query A operand: row n = (h, g) = (n >> 2, n & 3), nonzero only where
     // g == jq: 32 dims of group jq of head h.
     const half_t* qh = a.q + ((int64_t)b * a.n_q_heads + kvh * GQ) * D;
@@ -756,8 +758,8 @@ int64_t stream_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_
 int stream_launch(const void* query, const void* k_data, const void* v_data, const void* k_scale, const void* v_scale,
                   const int32_t* block_table, const int32_t* seq_lens, void* output, int32_t output_is_f32,
                   void* workspace, int64_t workspace_bytes_avail, int64_t batch, int64_t num_q_heads,
-                  int64_t num_kv_heads, int64_t head_dim, int64_t max_pages, float softmax_scale, int32_t chunk_tiles,
-                  int32_t max_chunks, void* stream) {
+                  int64_t num_kv_heads, int64_t head_dim, int64_t max_pages, int64_t bt_cols, int32_t page_shift,
+                  float softmax_scale, int32_t chunk_tiles, int32_t max_chunks, void* stream) {
     if (!stream_supported(num_q_heads, num_kv_heads, head_dim)) return kInvalidArgument;
     if (chunk_tiles <= 0 || chunk_tiles > st::kMaxChunkTiles || max_chunks <= 0 || max_chunks > st::kMaxChunks)
         return kInvalidArgument;
@@ -777,6 +779,8 @@ int stream_launch(const void* query, const void* k_data, const void* v_data, con
     a.batch = (int)batch;
     a.n_q_heads = (int)num_q_heads;
     a.max_pages = (int)max_pages;
+    a.bt_cols = (int)bt_cols;
+    a.page_shift = page_shift;
     a.max_chunks = max_chunks;
     a.chunk_tiles = chunk_tiles;
     a.log2_scale = softmax_scale * 1.4426950408889634f;

@@ -37,7 +37,9 @@ __all__ = ["fused_int4_paged_decode_attention", "_int4_paged_decode_attention", 
 def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, max_pages: int,
                 total_tokens: int = -1, max_tokens: int = -1, tokens_per_split: int = 0,
                 waves_per_block: int = 0) -> tuple[int, int, int, int]:
-    """(chunk_tiles, max_chunks, waves_per_block, workspace_bytes) from iris_decode_plan."""
+    """(chunk_tiles, max_chunks, waves_per_block, workspace_bytes) from iris_decode_plan.
+
+    ``max_pages`` counts 16-token pages: block_table columns * page_size // 16."""
     ct, mc, nw = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
     ws = ctypes.c_int64()
     status = _lib.lib().iris_decode_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages,
@@ -153,8 +155,15 @@ def _launch_decode(query, k_data, v_data, k_scale, v_scale, block_table, seq_len
     _lib.check(status, "iris_int4_paged_decode_attention")
 
 
+# Scope of the INT4 decode beyond the reference's fused path (page_size 16,
+# head_dim 64/128, at most 16 query heads per kv head: fused_attention.py:
+# 390-403): pages of 16 << k tokens, head_dim 256, any GQA ratio.
+INT4_PAGE_SIZES = (16, 32, 64, 128, 256)
+INT4_HEAD_DIMS = (64, 128, 256)
+
+
 def _validate_common_decode_inputs(query, block_table, seq_lens, *, num_pages: int,
-                                   num_kv_heads: int, page_size: int):
+                                   num_kv_heads: int, page_size: int, int4: bool = False):
     """Checks of fused_attention.py:373-434, same order and types; the
     per-sequence page-id loop is one vectorised check.  Returns
     (batch, num_q_heads, head_dim, total_tokens, max_tokens)."""
@@ -166,24 +175,35 @@ def _validate_common_decode_inputs(query, block_table, seq_lens, *, num_pages: i
         raise ValueError("query must have shape [B, Hq, D]")
     if query.dtype != torch.float16:
         raise TypeError("query must use FP16(torch.float16)")
-    if page_size != 16:
-        raise NotImplementedError("decode fast path currently supports page_size=16")
+    if page_size not in (INT4_PAGE_SIZES if int4 else (16,)):
+        raise NotImplementedError("decode fast path currently supports page_size="
+                                  + ("16 << k (16-256)" if int4 else "16"))
     batch, num_query_heads, head_dim = query.shape
-    if head_dim not in (64, 128):
-        raise NotImplementedError("decode fast path currently supports head_dim in {64, 128}")
+    if head_dim not in (INT4_HEAD_DIMS if int4 else (64, 128)):
+        raise NotImplementedError("decode fast path currently supports head_dim in "
+                                  + ("{64, 128, 256}" if int4 else "{64, 128}"))
     if num_query_heads % num_kv_heads != 0:
         raise ValueError("num_query_heads must be divisible by num_kv_heads")
-    if num_query_heads // num_kv_heads > 16:
+    if not int4 and num_query_heads // num_kv_heads > 16:
         raise NotImplementedError("decode fast path supports at most 16 query heads per KV head")
     if block_table.ndim != 2 or block_table.shape[0] != batch:
         raise ValueError("block_table must have shape [B, max_pages_per_sequence]")
     if seq_lens.shape != (batch,):
         raise ValueError("seq_lens must have shape [B]")
-    if block_table.dtype != torch.int32 or seq_lens.dtype != torch.int32:
-        raise TypeError("block_table and seq_lens must use torch.int32")
+    # int64 metadata is accepted, as the eager path accepts it
+    # (torch_eager_attention.py:130-133; the reference's fused path takes
+    # int32 only, fused_attention.py:409-410).
+    if block_table.dtype not in (torch.int32, torch.int64) or seq_lens.dtype not in (torch.int32, torch.int64):
+        raise TypeError("block_table and seq_lens must use torch.int32 or torch.int64")
     device = query.device
     if block_table.device != device or seq_lens.device != device:
         raise ValueError("block_table and seq_lens must be on the query device")
+    if block_table.dtype == torch.int64:
+        # ids outside the pool stay outside it (-1 or num_pages), so the
+        # device check below reports them as the reference does
+        block_table = block_table.clamp(-1, num_pages).to(torch.int32)
+    if seq_lens.dtype == torch.int64:
+        seq_lens = seq_lens.clamp(-1, 2 ** 31 - 1).to(torch.int32)
     max_pages = block_table.shape[1]
     # The per-sequence checks of fused_attention.py:415-429 (lengths
     # positive, enough pages, page ids inside the pool) in one device
@@ -252,7 +272,7 @@ def fused_int4_paged_decode_attention(
         raise ValueError("packed cache shape does not match query/page_size")
     batch, num_q_heads, head_dim, total, longest, block_table, seq_lens = _validate_common_decode_inputs(
         query, block_table, seq_lens, num_pages=num_pages, num_kv_heads=num_kv_heads,
-        page_size=page_size)
+        page_size=page_size, int4=True)
     scale_shape = (num_pages, page_size, num_kv_heads, head_dim // group_size)
     if tuple(k_scale.shape) != scale_shape:
         raise ValueError(f"k_scale must have shape {scale_shape}")
@@ -276,7 +296,7 @@ def fused_int4_paged_decode_attention(
     if batch == 0:
         return output
     scale = _qk_scale(head_dim, softmax_scale)
-    plan = decode_plan(batch, num_q_heads, num_kv_heads, head_dim, block_table.shape[1],
+    plan = decode_plan(batch, num_q_heads, num_kv_heads, head_dim, block_table.shape[1] * (page_size // 16),
                        total, longest, tokens_per_split, waves_per_block)
     _launch_decode(_dense(query, 16), k_data, v_data, k_scale, v_scale, block_table, seq_lens, output,
                    scale, plan, workspace)
@@ -297,7 +317,8 @@ def _int4_paged_decode_attention(query, k_data, v_data, k_scale, v_scale, block_
     if batch == 0:
         return
     scale = _qk_scale(head_dim, softmax_scale)
-    plan = decode_plan(batch, num_q_heads, k_data.shape[2], head_dim, block_table.shape[1])
+    plan = decode_plan(batch, num_q_heads, k_data.shape[2], head_dim,
+                       block_table.shape[1] * (k_data.shape[1] // 16))
     _launch_decode(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, scale,
                    plan)
 

@@ -62,9 +62,11 @@ def test_decode_rejects_unsupported_shapes_before_launch():
                                                     null, 0, a["B"], a["Hq"], a["Hkv"], a["D"], a["P"],
                                                     a["NP"], a["maxP"], ctypes.c_float(0.1), a["ct"],
                                                     a["mc"], a["nw"], null)
-    assert call(P=32) == 1          # page_size must be 16
-    assert call(D=96) == 1          # head_dim in {64, 128}
-    assert call(Hq=34, Hkv=2) == 1  # more than 16 query heads per kv head
+    assert call(P=48) == 1          # page_size must be 16 << k
+    assert call(P=8) == 1
+    assert call(P=512) == 1
+    assert call(D=96) == 1          # head_dim in {64, 128, 256}
+    assert call(D=512) == 1
     assert call(Hq=9) == 1          # Hq not divisible by Hkv
     assert call(ct=1, mc=1) == 1    # chunks do not cover max_pages
     assert call(nw=5) == 1

@@ -344,13 +344,37 @@ def test_validation_errors(device):
     with pytest.raises(IndexError):
         fused_int4_paged_decode_attention(q, *gpu, bad_bt, sl)
     with pytest.raises(TypeError):
-        fused_int4_paged_decode_attention(q, *gpu, bt.long(), sl)
+        fused_int4_paged_decode_attention(q, *gpu, bt.to(torch.int16), sl)
     with pytest.raises(TypeError):
         fused_int4_paged_decode_attention(q.float(), *gpu, bt, sl)
+    # int64 ids and lengths past the int32 range are still invalid, as in the reference
+    huge_bt = bt.long()
+    huge_bt[1, 0] = 2 ** 32 + 1  # would wrap to page 1 if narrowed naively
+    with pytest.raises(IndexError):
+        fused_int4_paged_decode_attention(q, *gpu, huge_bt, sl.long())
+    huge_sl = sl.long()
+    huge_sl[0] = 2 ** 40
+    with pytest.raises(ValueError):
+        fused_int4_paged_decode_attention(q, *gpu, bt.long(), huge_sl)
     with pytest.raises(NotImplementedError):
         fused_int4_paged_decode_attention(q, *gpu, bt, sl, group_size=64)
     with pytest.raises(ValueError):
         fused_int4_paged_decode_attention(q, *gpu, bt, sl, torch.empty(1, device=device))
+
+
+@pytest.mark.parametrize("cfg", [1, 3])
+def test_int64_metadata_matches_int32(device, cfg):
+    # int64 block_table / seq_lens, accepted like the eager path
+    # (torch_eager_attention.py:130-133): the same result as int32.
+    case, cpu, gpu = prepared(cfg, device)
+    q, bt, sl = to(device, case.query, case.block_table, case.seq_lens)
+    want = torch.empty(q.shape, dtype=torch.float32, device=device)
+    fused_int4_paged_decode_attention(q, *gpu, bt, sl, want)
+    for bt_x, sl_x in ((bt.long(), sl.long()), (bt.long(), sl), (bt, sl.long())):
+        got = torch.empty_like(want)
+        fused_int4_paged_decode_attention(q, *gpu, bt_x, sl_x, got)
+        torch.cuda.synchronize(device)
+        assert torch.equal(got, want)
 
 
 def test_hip_graph_replay(device):
@@ -376,3 +400,52 @@ def test_hip_graph_replay(device):
         graph.replay()
         torch.cuda.synchronize(device)
         assert torch.equal(out, eager), f"replay {i}"
+
+
+# ------------------------------------------------------------------ wider scope
+def _quantized_pool(num_pages, page_size, hkv, d, gen):
+    """A cache pool of random fp16 K/V quantised as the append writes it."""
+    from oracle.torch_eager_kv import pack_int4, quantize_int4_groupwise
+    out = []
+    for _ in range(2):
+        x = (torch.randn(num_pages, page_size, hkv, d, generator=gen) * 1.5).to(torch.float16)
+        codes, scales = quantize_int4_groupwise(x, 32)
+        out.append((pack_int4(codes), scales))
+    (kd, ks), (vd, vs) = out
+    return kd, vd, ks, vs
+
+
+@pytest.mark.parametrize("kernel", list(KERNELS))
+@pytest.mark.parametrize("hq,hkv,d,page,lens,tps", [
+    (16, 4, 256, 16, [1, 300, 1000], 0),        # head_dim 256
+    (16, 4, 256, 16, [700, 1200], 128),
+    (32, 1, 128, 16, [50, 900, 2000], 0),       # 32 query heads per kv head
+    (48, 2, 64, 16, [333, 1500], 256),          # 24 per kv head: a full and a half block
+    (20, 1, 128, 16, [77, 555], 0),
+    (32, 8, 128, 32, [40, 1000, 3000], 0),      # 32-token pages
+    (32, 8, 128, 32, [2100, 3000], 256),
+    (8, 2, 128, 64, [1, 100, 700], 0),          # 64-token pages
+    (16, 4, 64, 128, [130, 5000], 512),         # 128-token pages
+    (32, 8, 128, 256, [4000, 17], 0),           # 256-token pages
+])
+def test_wider_scope_matches_eager(device, kernel, hq, hkv, d, page, lens, tps):
+    # Shapes the reference's fused decode rejects (fused_attention.py:390-403)
+    # and its eager path computes: held to the same tolerance.
+    log(f"decode scope: Hq={hq} Hkv={hkv} D={d} P={page} lens={lens} split={tps} kernel={kernel}")
+    g = torch.Generator().manual_seed(hq * 7 + d + page + len(lens))
+    B = len(lens)
+    max_pages = max(-(-n // page) for n in lens) + 1
+    num_pages = B * max_pages + 2
+    kd, vd, ks, vs = _quantized_pool(num_pages, page, hkv, d, g)
+    bt = torch.randperm(num_pages, generator=g)[: B * max_pages].view(B, max_pages).to(torch.int32)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(torch.float16)
+    want = torch_eager_int4_paged_decode_attention(q, kd, vd, ks, vs, bt, sl, page_size=page,
+                                                   out_dtype=torch.float32)
+    qg, btg, slg = to(device, q, bt, sl)
+    cache = to(device, kd, vd, ks, vs)
+    out = torch.empty(q.shape, dtype=torch.float32, device=device)
+    fused_int4_paged_decode_attention(qg, *cache, btg, slg, out, page_size=page, tokens_per_split=tps,
+                                      waves_per_block=KERNELS[kernel])
+    torch.cuda.synchronize(device)
+    assert_attention_close(out, want, f"Hq={hq} Hkv={hkv} D={d} P={page}")

@@ -201,7 +201,9 @@ def test_fp16_validation_errors(device):
     with pytest.raises(TypeError):
         fused_fp16_paged_decode_attention(q, kc.float(), vc.float(), bt, sl)
     with pytest.raises(TypeError):
-        fused_fp16_paged_decode_attention(q, kc, vc, bt.long(), sl)
+        fused_fp16_paged_decode_attention(q, kc, vc, bt.to(torch.int16), sl)
+    want = fused_fp16_paged_decode_attention(q, kc, vc, bt, sl)  # int64 metadata: the same result
+    assert torch.equal(fused_fp16_paged_decode_attention(q, kc, vc, bt.long(), sl.long()), want)
     with pytest.raises(ValueError):  # the cache's page dimension is checked first
         fused_fp16_paged_decode_attention(q, kc, vc, bt, sl, page_size=32)
     np_, _, hkv, d = kc.shape

@@ -59,7 +59,8 @@ def symbols(asm: str) -> list[str]:
 
 def test_every_layout_is_compiled(asm):
     assert sorted((int(d), int(k)) for _, d, k in symbols(asm)) == [(64, 1), (64, 2), (64, 4),
-                                                                    (128, 1), (128, 2), (128, 4)]
+                                                                    (128, 1), (128, 2), (128, 4),
+                                                                    (256, 1)]
 
 
 def test_tile_loop_waits_only_at_the_tile_boundary(asm):
