@@ -28,9 +28,11 @@ paged decode attention over the 4096 tokens.
 * ``fp16_decode``: the same decode over an fp16 cache (the reference's
   matched FP16 baseline), timed the same way; ``int4_speedup`` is its time
   over the INT4 decode's.
-* ``cpu_baseline``: the checker's restatement of the reference's PyTorch
-  eager decode (oracle/torch_eager_attention.py), timed on this host's
-  cores on a bounded sample of the same workload.
+* ``cpu_baseline``: the checker's restatements of the reference's PyTorch
+  eager decode and append (oracle/), timed on this host's cores on bounded
+  samples of the same workloads (decode GB/s as ``value``; the step's
+  append and a sample of the configuration-5 bulk append in tokens/s), with
+  the host's CPU model.
 
 --gpus N > 1 exits: this path is measured on one GPU.
 """
@@ -70,8 +72,13 @@ def append_bytes(n_tok, n_kv, d, n_pos) -> int:
 
 
 def decode_kernel_name(plan, group: int, n_kv: int, d: int, batch: int, max_pages: int) -> str:
-    """Name of the decode kernel a plan runs, as rocprofv3 reports it: the
-    page-streaming kernel for 16-wave plans, the general kernel otherwise."""
+    """Name of the decode kernel a plan runs, as rocprofv3 reports it.  16-wave
+    plans: the streaming kernel for its shape (D=128, Hkv=8, 4 query heads per
+    kv head) in chunk mode with at most 64 chunks, else the page-streaming
+    kernel; other plans: the general kernel."""
+    if (plan[2] == 16 and plan[0] > 0 and plan[1] <= 64 and d == 128 and n_kv == 8 and group == 4
+            and os.environ.get("IRIS_DECODE_KERNEL") != "pages"):
+        return "void iris::st::int4_decode_stream_kernel<8>(iris::st::Args)"
     if plan[2] == 16:
         gs = 4
         while gs > 1 and gs * group > 16:
@@ -385,40 +392,81 @@ def main() -> int:
     # ------------------------------------------------ CPU baseline (port)
     if not args.no_cpu_baseline:
         from oracle.torch_eager_attention import torch_eager_int4_paged_decode_attention
+        from oracle.torch_eager_kv import torch_eager_append
 
         threads = os.cpu_count() or 1
         torch.set_num_threads(threads)
-        sample = args.cpu_sample or min(B, 8)
         cpu_cache = tuple(t.cpu() for t in caches[0])
+
+        def timed(fn, runs=5, budget_s=8.0):
+            fn()  # warm-up
+            times, t_end = [], time.perf_counter() + budget_s
+            for _ in range(runs):
+                t1 = time.perf_counter()
+                fn()
+                times.append(time.perf_counter() - t1)
+                if time.perf_counter() > t_end:
+                    break
+            return statistics.median(times), len(times)
+
+        # decode: as many of the B sequences as ~2 s a run allows (at least 4)
+        t1 = time.perf_counter()
+        torch_eager_int4_paged_decode_attention(case.query[:1], *cpu_cache, case.block_table[:1], case.seq_lens[:1])
+        per_seq = time.perf_counter() - t1
+        sample = args.cpu_sample or max(4, min(B, int(2.0 / max(per_seq, 1e-6))))
         q_s, bt_s, sl_s = case.query[:sample], case.block_table[:sample], case.seq_lens[:sample]
-        torch_eager_int4_paged_decode_attention(q_s, *cpu_cache, bt_s, sl_s)  # warm-up
-        times = []
-        budget = time.perf_counter()
         ref = None
-        for _ in range(5):
-            t1 = time.perf_counter()
+
+        def cpu_decode():
+            nonlocal ref
             ref = torch_eager_int4_paged_decode_attention(q_s, *cpu_cache, bt_s, sl_s)
-            times.append(time.perf_counter() - t1)
-            if time.perf_counter() - budget > 25:
-                break
-        cpu_s = statistics.median(times)
+
+        cpu_s, n_dec = timed(cpu_decode)
         sbytes = decode_bytes(sample, Hq, Hkv, D, lens[:sample])
         # the GPU output of the last decode on replica 0 for the same sequences
         do_decode(0)
         torch.cuda.synchronize()
         err = (out[:sample].float().cpu() - ref.float()).abs().max().item()
+
+        # append, the step's: one new token per sequence into the cache
+        step_args = [t.cpu() for t in (new_k, new_v, new_pos, new_slots, cos, sin)]
+        app_cpu_s, n_app = timed(lambda: torch_eager_append(*step_args, *cpu_cache, rotary_dim=D, group_size=32,
+                                                            page_size=16), runs=20)
+        # bulk append (configuration 5), a bounded sample of its tokens
+        ac = workloads.append_case(5)
+        bulk_n = min(ac.key.shape[0], 4096)
+        bpool = ac.empty_cache(torch.device("cpu"), fill="zeros")
+        bargs = (ac.key[:bulk_n], ac.value[:bulk_n], ac.positions[:bulk_n], ac.slot_mapping[:bulk_n], ac.cos, ac.sin)
+        bulk_cpu_s, n_bulk_cpu = timed(lambda: torch_eager_append(*bargs, *bpool, rotary_dim=128, group_size=32,
+                                                                  page_size=16))
+        cpu_model = "unknown"
+        try:
+            for line in Path("/proc/cpuinfo").read_text().splitlines():
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
         result["cpu_baseline"] = {
             "value": round(sbytes / cpu_s / 1e9, 3),
             "unit": "GB/s",
             "cores": torch.get_num_threads(),
             "kind": "port",
+            "cpu_model": cpu_model,
             "sample": f"decode of the first {sample} of {B} sequences (L={lens[0]}) with the torch "
-                      f"restatement of torch_eager_int4_paged_decode_attention; median of {len(times)} runs "
-                      f"= {cpu_s * 1e3:.1f} ms",
+                      f"restatement of torch_eager_int4_paged_decode_attention, median of {n_dec} runs "
+                      f"= {cpu_s * 1e3:.1f} ms; append: the step's {B}-token append (median of {n_app} runs) "
+                      f"and the first {bulk_n} of configuration 5's {ac.key.shape[0]} bulk-append tokens "
+                      f"(median of {n_bulk_cpu}), with the restatement of torch_eager_append",
             "decode_us_equiv_full_batch": round(cpu_s * 1e6 * B / sample, 1),
             "gpu_vs_eager_max_abs_err": err,
+            "append_tokens_per_s": round(B / app_cpu_s, 1),
+            "append_us": round(app_cpu_s * 1e6, 1),
+            "bulk_append_tokens_per_s": round(bulk_n / bulk_cpu_s, 1),
         }
-        log(f"cpu baseline: {sbytes / cpu_s / 1e9:.3f} GB/s on {threads} threads; GPU vs eager max-abs err {err:.2e}")
+        log(f"cpu baseline ({cpu_model}, {threads} threads): decode {sbytes / cpu_s / 1e9:.3f} GB/s "
+            f"({sample} sequences), append {B / app_cpu_s:.0f} tok/s, bulk append {bulk_n / bulk_cpu_s:.0f} tok/s; "
+            f"GPU vs eager max-abs err {err:.2e}")
 
     print(json.dumps(result), flush=True)
     return 0
