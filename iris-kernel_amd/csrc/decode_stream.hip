@@ -682,7 +682,8 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(Args a)
     // Merge the M = n_chunks partials, each thread a float4 of the output:
     // o = sum_c w_c (o / l)_c / sum_c w_c with w_c = l_c 2^(m_c - m*), the
     // partials and their (m, l) loaded together, kMergeBatch chunks at a
-    // time, m* the running maximum.
+    // time, m* the running maximum.  This chunk's own partial comes from LDS
+    // (the same values it published).
     const int M = n_chunks;
     const auto ro = buf_rsrc(a.part_o + row0 * total, part_o * (uint32_t)M);
     const auto rm = buf_rsrc(a.part_ml + row0 * hq * 2, part_ml * (uint32_t)M);
@@ -695,9 +696,15 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(Args a)
             float2v_t ml[kMergeBatch];
 #pragma unroll
             for (int cb = 0; cb < kMergeBatch; ++cb) {
-                const uint32_t c = (uint32_t)min(c0 + cb, M - 1);
-                oc[cb] = load4_sc1(ro, c * part_o + (uint32_t)e4 * 16);
-                ml[cb] = load2_sc1(rm, (c * (uint32_t)hq + (uint32_t)h) * 8);
+                const int c = min(c0 + cb, M - 1);
+                if (c != chunk) {
+                    oc[cb] = load4_sc1(ro, (uint32_t)c * part_o + (uint32_t)e4 * 16);
+                    ml[cb] = load2_sc1(rm, ((uint32_t)c * (uint32_t)hq + (uint32_t)h) * 8);
+                } else {
+                    float m, l;
+                    oc[cb] = chunk4(e4, m, l);
+                    ml[cb] = float2v_t{m, l};
+                }
             }
             // past M: a repeat of partial M - 1 with weight 0
             float mb = mstar;
