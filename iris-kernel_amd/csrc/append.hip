@@ -34,6 +34,20 @@
 
 namespace iris {
 
+// Lane `i` of this lane's quad (DPP quad_perm broadcast).
+__device__ __forceinline__ uint32_t quad_lane(uint32_t x, int i) {
+    switch (i) {
+        case 1: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x55, 0xF, 0xF, true);
+        case 2: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xAA, 0xF, 0xF, true);
+        default: return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xFF, 0xF, 0xF, true);
+    }
+}
+// The value of the lane 4 above this one in its 16-lane row (DPP row_shl:4;
+// used where that lane is in the same append row).
+__device__ __forceinline__ uint32_t next_quad(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x104, 0xF, 0xF, true);
+}
+
 // RPT rows per thread: rows k * kRowsPerBlock + (thread's row) of the
 // block's RPT * kRowsPerBlock, every load of all RPT rows issued before the
 // first use (the slot, position, K and V loads together, then the RoPE rows),
@@ -144,15 +158,25 @@ __global__ __launch_bounds__(256) void rope_int4_paged_append_kernel(
         const uint32_t kword = pack_group8(kr, (float)ks16);
         const uint32_t vword = pack_group8(vr, (float)vs16);
 
-        if (live[k] && slot[k] >= 0) {
+        // 128-bit code stores: the first lane of each quad (one 32-dim group)
+        // gathers the quad's four words; 32-bit scale stores: the first lane
+        // of every other quad pairs its group's scale with the next group's.
+        const u32x4_t kq = {kword, quad_lane(kword, 1), quad_lane(kword, 2), quad_lane(kword, 3)};
+        const u32x4_t vq = {vword, quad_lane(vword, 1), quad_lane(vword, 2), quad_lane(vword, 3)};
+        const uint32_t ks = as_u32(half2_t{ks16, ks16});
+        const uint32_t vs = as_u32(half2_t{vs16, vs16});
+        const uint32_t ks2 = (ks & 0xFFFFu) | (next_quad(ks) << 16);
+        const uint32_t vs2 = (vs & 0xFFFFu) | (next_quad(vs) << 16);
+        if (live[k] && slot[k] >= 0 && (c & 3) == 0) {
             const int64_t page = slot[k] / page_size;
             const int64_t off = slot[k] - page * page_size;
             const int64_t cache_row = (page * page_size + off) * n_heads + head[k];
-            k_data[cache_row * chunks + c] = kword;  // D/2 bytes per row = `chunks` words
-            v_data[cache_row * chunks + c] = vword;
-            if ((c & 3) == 0) {
-                k_scale[cache_row * (head_dim >> 5) + (c >> 2)] = ks16;
-                v_scale[cache_row * (head_dim >> 5) + (c >> 2)] = vs16;
+            // D/2 bytes per row = chunks / 4 16-byte groups
+            reinterpret_cast<u32x4_t*>(k_data)[cache_row * (chunks >> 2) + (c >> 2)] = kq;
+            reinterpret_cast<u32x4_t*>(v_data)[cache_row * (chunks >> 2) + (c >> 2)] = vq;
+            if ((c & 7) == 0) {  // D/32 scales per row, two per 32-bit word
+                reinterpret_cast<uint32_t*>(k_scale)[(cache_row * (head_dim >> 5) + (c >> 2)) >> 1] = ks2;
+                reinterpret_cast<uint32_t*>(v_scale)[(cache_row * (head_dim >> 5) + (c >> 2)) >> 1] = vs2;
             }
         }
     }
