@@ -75,7 +75,8 @@ def decode_kernel_name(plan, group: int, n_kv: int, d: int, batch: int, max_page
     """Name of the decode kernel a plan runs, as rocprofv3 reports it.  16-wave
     plans: the streaming kernel for its shape (D=128, Hkv=8, 4 query heads per
     kv head) in chunk mode with at most 64 chunks, else the page-streaming
-    kernel; other plans: the general kernel."""
+    kernel; other plans: the general kernel (its VALU-tile variant with
+    IRIS_DECODE_KERNEL=valu)."""
     if (plan[2] == 16 and plan[0] > 0 and plan[1] <= 64 and d == 128 and n_kv == 8 and group == 4
             and os.environ.get("IRIS_DECODE_KERNEL") != "pages"):
         return "void iris::st::int4_decode_stream_kernel<8>(iris::st::Args)"
@@ -85,7 +86,10 @@ def decode_kernel_name(plan, group: int, n_kv: int, d: int, batch: int, max_page
             gs //= 2
         gs = min(gs, d // 32)
         return f"void iris::pg::int4_decode_pages_kernel<{d}, {gs}, {n_kv}>(iris::pg::Args)"
-    return f"void iris::int4_decode_kernel<{d}, {kernel_kvw(group, n_kv, batch, max_pages)}>(iris::DecodeArgs)"
+    kvw = kernel_kvw(group, n_kv, batch, max_pages)
+    if os.environ.get("IRIS_DECODE_KERNEL") == "valu":  # the VALU tile, measured against the MFMA one
+        return f"void iris::int4_decode_valu_kernel<{d}, {kvw}>(iris::DecodeArgs)"
+    return f"void iris::int4_decode_kernel<{d}, {kvw}>(iris::DecodeArgs)"
 
 
 def kernel_kvw(group: int, n_kv: int, batch: int, max_pages: int) -> int:

@@ -26,6 +26,44 @@ enum Status : int {
 __device__ __forceinline__ half2_t as_half2(uint32_t x) { return __builtin_bit_cast(half2_t, x); }
 __device__ __forceinline__ uint32_t as_u32(half2_t x) { return __builtin_bit_cast(uint32_t, x); }
 __device__ __forceinline__ uint32_t as_u32(float x) { return __builtin_bit_cast(uint32_t, x); }
+// (By value: __builtin_bit_cast applied directly to an element of an
+// ext_vector_type value, x[k], reads element 0 with hipcc 7.2's clang.)
+__device__ __forceinline__ float as_f32(uint32_t x) { return __builtin_bit_cast(float, x); }
+
+// Maximum / sum over the 16 lanes of a row (DPP: xor 1, xor 2, then the
+// half-row and row mirrors).
+__device__ __forceinline__ float dpp_f(float x, int ctrl) {
+    switch (ctrl) {
+        case 0: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true));
+        case 1: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true));
+        case 2: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true));
+        default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, true));
+    }
+}
+// Row maximum as four fused DPP maxima (v_max_f32_dpp; a VGPR a VALU
+// instruction wrote is read through DPP two wait states later).  NaN
+// operands follow v_max_f32: the other operand is returned.
+__device__ __forceinline__ float row16_max(float x) {
+    float y;
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "s_nop 1\n\t"
+        "v_max_f32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1"
+        : "=&v"(y)
+        : "v"(x));
+    return y;
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f(x, 0);
+    x += dpp_f(x, 1);
+    x += dpp_f(x, 2);
+    return x + dpp_f(x, 3);
+}
 
 // Split-KV arrival counters.  Every decode kernel keeps them in one region
 // at the head of its workspace, kCountersPerSeq uint32 per sequence

@@ -178,6 +178,129 @@ __device__ __forceinline__ void transpose_rows4(u32x4_t& x) {
     x = u32x4_t{x0, x1, x2, x3};
 }
 
+// ---- VALU tile: v_dot2c_f32_f16 with DPP row broadcasts (no MFMA)
+//
+// The alternative to the MFMA tile, selected at run time (IRIS_DECODE_KERNEL
+// = valu) for the layouts KVW * g = 16 with g = 4 or 16.  Every dot product
+// is a chain of v_dot2c_f32_f16 whose first operand is broadcast from one
+// lane of the 16-lane row (DPP row_newbcast), so each fp16 pair is unpacked
+// or computed once and no operand is replicated in registers:
+//   QK: the K codes stay in the MFMA A layout (lane = token n of the
+//       16-token half, row jq = 8-dim chunk of each group); the q pairs of
+//       the row's chunk sit one per lane (lane 4b + p: pair p of column
+//       4a + b, register a), and the partial sums of the four chunks are
+//       added across the rows with a 4 x 4 transpose;
+//   softmax / PV: lane (n, row rho) holds token n (and 16 + n) of columns
+//       col(rho, w), w = 0..3; PV broadcasts p * v_scale of token pair
+//       (t, t + 16) from lane t to the 16 lanes of the row, each of which
+//       accumulates the two dims of one V byte.
+// Instruction counts per 32-token tile and kv head equal the minimum g * D / 4
+// dot2 per product (QK and PV each) plus the unpacking and the reductions.
+
+// QK of column quad A over this lane's code pairs kp (the four pairs of one
+// k_operand dword): acc[b] = offset term of column 4A + b (broadcast from lane
+// 4A + b of qc) + sum_p kp[p] . (q pair broadcast from lane 4b + p of qv).
+// A VGPR a VALU instruction wrote is read through DPP two wait states later
+// (the leading s_nop).
+template <int A>
+__device__ __forceinline__ void qk_valu(float (&acc)[4], uint32_t qv, uint32_t qc, const u32x4_t kp) {
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_mov_b32_dpp %0, %5 row_newbcast:%10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mov_b32_dpp %1, %5 row_newbcast:%11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mov_b32_dpp %2, %5 row_newbcast:%12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_mov_b32_dpp %3, %5 row_newbcast:%13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %0, %4, %6 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %1, %4, %6 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %2, %4, %6 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %3, %4, %6 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %0, %4, %7 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %1, %4, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %2, %4, %7 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %3, %4, %7 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %0, %4, %8 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %1, %4, %8 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %2, %4, %8 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %3, %4, %8 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %0, %4, %9 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %1, %4, %9 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %2, %4, %9 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %3, %4, %9 row_newbcast:15 row_mask:0xf bank_mask:0xf"
+        : "=&v"(acc[0]), "=&v"(acc[1]), "=&v"(acc[2]), "=&v"(acc[3])
+        : "v"(qv), "v"(qc), "v"(kp[0]), "v"(kp[1]), "v"(kp[2]), "v"(kp[3]), "n"(4 * A), "n"(4 * A + 1),
+          "n"(4 * A + 2), "n"(4 * A + 3));
+}
+__device__ __forceinline__ void qk_valu_quad(int a, float (&acc)[4], uint32_t qv, uint32_t qc, const u32x4_t kp) {
+    switch (a) {  // a is a constant in every unrolled use
+        case 0: qk_valu<0>(acc, qv, qc, kp); break;
+        case 1: qk_valu<1>(acc, qv, qc, kp); break;
+        case 2: qk_valu<2>(acc, qv, qc, kp); break;
+        default: qk_valu<3>(acc, qv, qc, kp); break;
+    }
+}
+
+// PV of token pairs T0 .. T0 + 3: o[w][e] += vl / vh[tt] . (p pair of column
+// w broadcast from lane T0 + tt), e = 0 the byte's low-nibble dim, 1 its
+// high-nibble dim (16x codes).
+template <int T0>
+__device__ __forceinline__ void pv_valu(float (&o)[4][2], const uint32_t (&pv)[4], const uint32_t (&vl)[4],
+                                        const uint32_t (&vh)[4]) {
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_dot2c_f32_f16_dpp %0, %8, %12 row_newbcast:%20 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %1, %8, %16 row_newbcast:%20 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %2, %9, %12 row_newbcast:%20 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %3, %9, %16 row_newbcast:%20 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %4, %10, %12 row_newbcast:%20 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %5, %10, %16 row_newbcast:%20 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %6, %11, %12 row_newbcast:%20 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %7, %11, %16 row_newbcast:%20 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %0, %8, %13 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %1, %8, %17 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %2, %9, %13 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %3, %9, %17 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %4, %10, %13 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %5, %10, %17 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %6, %11, %13 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %7, %11, %17 row_newbcast:%21 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %0, %8, %14 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %1, %8, %18 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %2, %9, %14 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %3, %9, %18 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %4, %10, %14 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %5, %10, %18 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %6, %11, %14 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %7, %11, %18 row_newbcast:%22 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %0, %8, %15 row_newbcast:%23 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %1, %8, %19 row_newbcast:%23 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %2, %9, %15 row_newbcast:%23 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %3, %9, %19 row_newbcast:%23 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %4, %10, %15 row_newbcast:%23 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %5, %10, %19 row_newbcast:%23 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %6, %11, %15 row_newbcast:%23 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %7, %11, %19 row_newbcast:%23 row_mask:0xf bank_mask:0xf"
+        : "+v"(o[0][0]), "+v"(o[0][1]), "+v"(o[1][0]), "+v"(o[1][1]), "+v"(o[2][0]), "+v"(o[2][1]),
+          "+v"(o[3][0]), "+v"(o[3][1])
+        : "v"(pv[0]), "v"(pv[1]), "v"(pv[2]), "v"(pv[3]), "v"(vl[0]), "v"(vl[1]), "v"(vl[2]), "v"(vl[3]),
+          "v"(vh[0]), "v"(vh[1]), "v"(vh[2]), "v"(vh[3]), "n"(T0), "n"(T0 + 1), "n"(T0 + 2), "n"(T0 + 3));
+}
+
+// Four transposed 8-byte LDS reads at addr + OFF + k * STRIDE (k = 0..3) that
+// wait for their own results (as lds_tr8).
+template <int OFF, int STRIDE>
+__device__ __forceinline__ void lds_tr8_x4(uint32_t addr, int2v_t (&w)[4]) {
+    static_assert(OFF >= 0 && OFF + 3 * STRIDE < 65536, "ds offset range");
+    asm volatile(
+        "ds_read_b64_tr_b8 %0, %4 offset:%5\n\t"
+        "ds_read_b64_tr_b8 %1, %4 offset:%6\n\t"
+        "ds_read_b64_tr_b8 %2, %4 offset:%7\n\t"
+        "ds_read_b64_tr_b8 %3, %4 offset:%8\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(w[0]), "=&v"(w[1]), "=&v"(w[2]), "=&v"(w[3])
+        : "v"(addr), "n"(OFF), "n"(OFF + STRIDE), "n"(OFF + 2 * STRIDE), "n"(OFF + 3 * STRIDE)
+        : "memory");
+}
+
 // Workgroups are dispatched round-robin over the 8 XCDs; renumber them so
 // that consecutive logical ids (the kv blocks and chunks of one sequence,
 // which share scale lines and block-table rows) run on the same XCD and L2.
@@ -296,9 +419,12 @@ struct DecodeLayout {
     static constexpr int NSO = 64 / (SSEG / 4) > 16 ? NS : 1;
 };
 
-template <int D, int KVW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void int4_decode_kernel(DecodeArgs a) {
+// The kernel body; VALU selects the v_dot2c tile instead of the MFMA tile
+// (the loads, the split and the merges are the same).
+template <int D, int KVW, bool VALU>
+__device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     using L = DecodeLayout<D, KVW>;
+    static_assert(!VALU || ((KVW == 4 || KVW == 1) && D != 256), "VALU tile: g = 4 (KVW 4) or g = 16 (KVW 1)");
     constexpr int G = L::G, HB = L::HB, C = L::C, SSEG = L::SSEG;
     static_assert(C >= 2 && (C & (C - 1)) == 0, "chunks per token must be a power of two >= 2");
     extern __shared__ __align__(16) uint8_t smem[];
@@ -544,6 +670,52 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
         o[grp][0] = o[grp][1] = float4_t{0, 0, 0, 0};
     }
 
+    // ---- VALU tile operands and state (VALU only).  The 16 columns are
+    // 4a + b; with KVW = 4 (g = 4) column 4a + b is query head b of kv head
+    // kv0 + a, with KVW = 1 (g = 16) query head 4a + b of kv head kv0.
+    //   qv[a][grp]: lane (n, row jq) holds q pair n & 3 (k_operand order) of
+    //     column 4a + (n >> 2), dims grp * 32 + 8 jq .. + 7;
+    //   qc[grp]: the +8 code offset term of column n over the same dims,
+    //     -8 * 2^-24 * sum q (the chain's start; the rows' partial sums add
+    //     up to qinit).
+    //   After QK, lane (n, row rho) holds tokens n and 16 + n of the columns
+    //   col(rho, w) = 4 rho + w (KVW = 4: the row is a kv head) or 4 w + rho
+    //   (KVW = 1), w = 0..3; softmax and PV keep that layout.
+    uint32_t qv[4][G], qc[G];
+    float vm[4], vl[4], vps[G][4], vo[G][4][2];
+    if constexpr (VALU) {
+        const half_t s16 = (half_t)0.0625f;
+#pragma unroll
+        for (int grp = 0; grp < G; ++grp) {
+            const u32x4_t w = qraw[grp];
+            const half2_t w0 = as_half2(w[0]), w1 = as_half2(w[1]), w2 = as_half2(w[2]), w3 = as_half2(w[3]);
+            const float part = (float)w0.x + (float)w2.x + (float)(w0.y * s16) * 16.0f + (float)(w2.y * s16) * 16.0f +
+                               (float)w1.x + (float)w3.x + (float)(w1.y * s16) * 16.0f + (float)(w3.y * s16) * 16.0f;
+            qc[grp] = as_u32(-8.0f * 5.9604644775390625e-08f * part);
+#pragma unroll
+            for (int qa = 0; qa < 4; ++qa) {
+                const int hqa = kv0 * g + 4 * qa + (n >> 2);
+                const u32x4_t x = *reinterpret_cast<const u32x4_t*>(a.q + ((int64_t)b * a.n_q_heads + hqa) * D + grp * 32 + jq * 8);
+                const half2_t x0 = as_half2(x[0]), x1 = as_half2(x[1]), x2 = as_half2(x[2]), x3 = as_half2(x[3]);
+                const half2_t pr[4] = {half2_t{x0.x, x2.x}, half2_t{x0.y * s16, x2.y * s16}, half2_t{x1.x, x3.x},
+                                       half2_t{x1.y * s16, x3.y * s16}};
+                const uint32_t lo = (n & 1) ? as_u32(pr[1]) : as_u32(pr[0]);
+                const uint32_t hi = (n & 1) ? as_u32(pr[3]) : as_u32(pr[2]);
+                qv[qa][grp] = (n & 2) ? hi : lo;
+            }
+        }
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            vm[w] = -INFINITY;
+            vl[w] = 0.0f;
+#pragma unroll
+            for (int grp = 0; grp < G; ++grp) {
+                vps[grp][w] = 0.0f;
+                vo[grp][w][0] = vo[grp][w][1] = 0.0f;
+            }
+        }
+    }
+
     // ---- compute one tile whose loads have landed.  The K registers are
     // consumed by QK; the next tile's K loads are issued right after, so they
     // fly during softmax and PV.
@@ -689,6 +861,167 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
         }
     };
 
+    // ---- the VALU tile (VALU only; the layouts above the q setup).
+    // V reads: supplier lane n of a row gives token T = (k & 1) + 16 ((k >> 1)
+    // & 1) + 2 (k >> 2), k = n >> 1 (plus 4 per read), half n & 1, so each
+    // dword of a read holds tokens (t, t + 1, t + 16, t + 17) and the code
+    // masks pair t with t + 16.  The chunk of (kv head x / G, group x % G)
+    // sits at position x ^ f(T) (f as for the loads above).
+    const int kv_row = KVW == 4 ? jq : 0;
+    const int vt_tok = ((n >> 1) & 1) + 16 * ((n >> 2) & 1) + 2 * (n >> 3);
+    const uint32_t vt_base = (uint32_t)vt_tok * (C * 16) +
+                             ((uint32_t)(((vt_tok & 3) | ((vt_tok >> 4) << 2)) & (C - 1)) << 4) + 8 * (n & 1);
+    const uint32_t valu_s_tok = (uint32_t)(n * KVW * G) * 2;  // token n's scales in a stage's scale block
+    auto compute_valu = [&](int tile, auto bufc, uint32_t (&kw)[2][L::KREGS], int next) {
+        constexpr int kBufOff = decltype(bufc)::value * L::BUF;
+        const uint8_t* const vb = stage + kBufOff;
+        const uint32_t sb = opaque(valu_s_tok);
+        const half_t* const ks_lds = reinterpret_cast<const half_t*>(vb + L::VBUF + sb);
+        const half_t* const vs_lds = reinterpret_cast<const half_t*>(vb + L::VBUF + L::SBUF + sb) + kv_row * G;
+        const int tok_base = tile * kTile;
+        const bool full = tok_base + kTile <= seq_len;
+        if constexpr (D == 128) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int j = 0; j < KVW; ++j) {
+                    u32x4_t x = {kw[r][j * G], kw[r][j * G + 1], kw[r][j * G + 2], kw[r][j * G + 3]};
+                    transpose_rows4(x);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) kw[r][j * G + q] = x[q];
+                }
+        }
+        // ---- QK per 16-token half: partial sums over this row's chunk,
+        // scaled per (token, group), then the four rows' partial sums added:
+        // sc[r][w] = score of token 16 r + n, column col(rho, w)
+        float sc[2][4];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            float sacc[4][4];
+#pragma unroll
+            for (int qa = 0; qa < 4; ++qa)
+#pragma unroll
+                for (int qb = 0; qb < 4; ++qb) sacc[qa][qb] = 0.0f;
+#pragma unroll
+            for (int grp = 0; grp < G; ++grp) {
+                u32x4_t kp1 = {0, 0, 0, 0};
+                if constexpr (KVW == 1) kp1 = __builtin_bit_cast(u32x4_t, k_operand(kw[r][grp]));
+#pragma unroll
+                for (int qa = 0; qa < 4; ++qa) {
+                    const int j = KVW == 4 ? qa : 0;
+                    const u32x4_t kp = KVW == 4 ? __builtin_bit_cast(u32x4_t, k_operand(kw[r][j * G + grp])) : kp1;
+                    float acc[4];
+                    qk_valu_quad(qa, acc, qv[qa][grp], qc[grp], kp);
+                    const float ks = (float)ks_lds[16 * r * KVW * G + j * G + grp];
+#pragma unroll
+                    for (int qb = 0; qb < 4; ++qb) sacc[qa][qb] = __builtin_fmaf(ks, acc[qb], sacc[qa][qb]);
+                    // in program order: unpacking every dword ahead of its
+                    // chain would hold 4 VGPRs per dword
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+#pragma unroll
+            for (int f = 0; f < 4; ++f) {
+                u32x4_t x;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) x[k] = as_u32(KVW == 4 ? sacc[k][f] : sacc[f][k]);
+                transpose_rows4(x);
+                sc[r][f] = (as_f32(x[0]) + as_f32(x[1])) + (as_f32(x[2]) + as_f32(x[3]));
+            }
+        }
+        if (next < t_end) issue_k(next, kw);
+        if (!full) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+                if (tok_base + 16 * r + n >= seq_len) {
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) sc[r][w] = -INFINITY;
+                }
+        }
+        // ---- online softmax per column (base 2, lazy rescale)
+        float mx[4];
+        bool grow = false;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            mx[w] = row16_max(fmaxf(sc[0][w], sc[1][w]));  // finite: token tile*32 < seq_len
+            grow = grow || mx[w] > vm[w] + lazy;
+        }
+        if (__ballot(grow) != 0) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float m_new = fmaxf(vm[w], mx[w]);
+                const float alpha = __builtin_amdgcn_exp2f((vm[w] - m_new) * c24);
+                vm[w] = m_new;
+                vl[w] *= alpha;
+#pragma unroll
+                for (int grp = 0; grp < G; ++grp) {
+                    vps[grp][w] *= alpha;
+                    vo[grp][w][0] *= alpha;
+                    vo[grp][w][1] *= alpha;
+                }
+            }
+        }
+        float p[2][4];
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float moff = -vm[w] * c24;
+#pragma unroll
+            for (int r = 0; r < 2; ++r) p[r][w] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[r][w], c24, moff));
+            vl[w] += p[0][w] + p[1][w];
+        }
+        // ---- PV: B pairs p * v_scale of tokens (n, 16 + n), rounded once to fp16
+        float vs0[G], vs1[G];
+#pragma unroll
+        for (int grp = 0; grp < G; ++grp) {
+            vs0[grp] = (float)vs_lds[grp];
+            vs1[grp] = (float)vs_lds[16 * KVW * G + grp];
+        }
+        if (!full) {
+            asm volatile("");  // a real branch (see compute)
+            if (tok_base + n >= seq_len) {
+#pragma unroll
+                for (int grp = 0; grp < G; ++grp) vs0[grp] = 0.0f;
+            }
+            if (tok_base + 16 + n >= seq_len) {
+#pragma unroll
+                for (int grp = 0; grp < G; ++grp) vs1[grp] = 0.0f;
+            }
+        }
+        const uint32_t stage_lds = (uint32_t)(uintptr_t)(const IRIS_LDS void*)stage;
+        const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+        for (int grp = 0; grp < G; ++grp) {
+            uint32_t pv[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const half2_t h = {(half_t)(p[0][w] * vs0[grp]), (half_t)(p[1][w] * vs1[grp])};
+                pv[w] = as_u32(h);
+                vps[grp][w] = __builtin_amdgcn_fdot2(h, one2, vps[grp][w], false);
+            }
+            int2v_t rd[4];
+            lds_tr8_x4<kBufOff, 4 * L::SEG>(stage_lds + (vt_base ^ ((uint32_t)(kv_row * G + grp) << 4)), rd);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t a0 = (uint32_t)rd[k][0], a8 = a0 >> 8, b0 = (uint32_t)rd[k][1], b8 = b0 >> 8;
+                const uint32_t vlo[4] = {(a0 ^ 0x00080008u) & 0x000F000Fu, (a8 ^ 0x00080008u) & 0x000F000Fu,
+                                         (b0 ^ 0x00080008u) & 0x000F000Fu, (b8 ^ 0x00080008u) & 0x000F000Fu};
+                const uint32_t vhi[4] = {(a0 ^ 0x00800080u) & 0x00F000F0u, (a8 ^ 0x00800080u) & 0x00F000F0u,
+                                         (b0 ^ 0x00800080u) & 0x00F000F0u, (b8 ^ 0x00800080u) & 0x00F000F0u};
+                switch (k) {  // k is a constant in every unrolled use
+                    case 0: pv_valu<0>(vo[grp], pv, vlo, vhi); break;
+                    case 1: pv_valu<4>(vo[grp], pv, vlo, vhi); break;
+                    case 2: pv_valu<8>(vo[grp], pv, vlo, vhi); break;
+                    default: pv_valu<12>(vo[grp], pv, vlo, vhi); break;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+    auto run_tile = [&](int tile, auto bufc, uint32_t (&kw)[2][L::KREGS], int next) {
+        if constexpr (VALU) compute_valu(tile, bufc, kw, next);
+        else compute(tile, bufc, kw, next);
+    };
+
     // Wave w takes tiles t_begin + w, + nw, ...: a fixed split, so every
     // run (and every HIP-graph replay) adds the same terms in the same order.
     // Two stage buffers with compile-time bases: the loop is unrolled by two.
@@ -696,36 +1029,64 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
         int next = tile + nw;
         wait_vmem_all();  // this tile's V, scales (LDS) and K (registers) have landed
         if (next < t_end) issue_v(next, 1);
-        compute(tile, std::integral_constant<int, 0>(), kw, next);
+        run_tile(tile, std::integral_constant<int, 0>(), kw, next);
         tile = next;
         if (tile >= t_end) break;
         next = tile + nw;
         wait_vmem_all();
         if (next < t_end) issue_v(next, 0);
-        compute(tile, std::integral_constant<int, 1>(), kw, next);
+        run_tile(tile, std::integral_constant<int, 1>(), kw, next);
         tile = next;
     }
-    m_run *= c24;  // back to base-2 logits for the merges
-
-    // ---- final per-lane values: undo the code offset and the 2^-24 units
-    l_part = row_sum4(l_part);
+    // ---- final per-lane values: undo the code offset and the 2^-24 units,
+    // back to base-2 logits for the merges
+    if constexpr (VALU) {
 #pragma unroll
-    for (int grp = 0; grp < G; ++grp) ps[grp] = 8.0f * row_sum4(ps[grp]);
+        for (int w = 0; w < 4; ++w) {
+            vm[w] *= c24;
+            vl[w] = row16_sum(vl[w]);
+#pragma unroll
+            for (int grp = 0; grp < G; ++grp) vps[grp][w] = 8.0f * row16_sum(vps[grp][w]);
+        }
+    } else {
+        m_run *= c24;
+        l_part = row_sum4(l_part);
+#pragma unroll
+        for (int grp = 0; grp < G; ++grp) ps[grp] = 8.0f * row_sum4(ps[grp]);
+    }
 
     // ---- merge the waves of this workgroup (LDS, MFMA C order: lane-major,
     // so stores and loads are free of bank conflicts)
     __syncthreads();  // every wave is done with its stage
     float* const mo = reinterpret_cast<float*>(smem + wave * L::WAVE_LDS);
+    if constexpr (VALU) {
+        // dim grp * 32 + 2 n + e of column col(jq, w), in C order
 #pragma unroll
-    for (int grp = 0; grp < G; ++grp)
+        for (int w = 0; w < 4; ++w) {
+            const int cw = KVW == 4 ? 4 * jq + w : 4 * w + jq;
 #pragma unroll
-        for (int e = 0; e < 2; ++e)
+            for (int grp = 0; grp < G; ++grp)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                mo[((grp * 2 + e) * 4 + i) * 64 + lane] = o[grp][e][i] * (e ? 1048576.0f : 16777216.0f) - ps[grp];
-    if (jq == 0) {
-        mo[16 * D + n] = m_run;
-        mo[16 * D + 16 + n] = l_part;
+                for (int e = 0; e < 2; ++e)
+                    mo[((grp * 2 + e) * 4 + (n & 3)) * 64 + 16 * (n >> 2) + cw] =
+                        vo[grp][w][e] * (e ? 1048576.0f : 16777216.0f) - vps[grp][w];
+            if (n == 0) {
+                mo[16 * D + cw] = vm[w];
+                mo[16 * D + 16 + cw] = vl[w];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int grp = 0; grp < G; ++grp)
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    mo[((grp * 2 + e) * 4 + i) * 64 + lane] = o[grp][e][i] * (e ? 1048576.0f : 16777216.0f) - ps[grp];
+        if (jq == 0) {
+            mo[16 * D + n] = m_run;
+            mo[16 * D + 16 + n] = l_part;
+        }
     }
     __syncthreads();
     // Every thread serves one column (threadIdx % 16) for all its elements.
@@ -848,6 +1209,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 
     }
 }
 
+template <int D, int KVW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void int4_decode_kernel(DecodeArgs a) {
+    decode_body<D, KVW, false>(a);
+}
+// The VALU tile (IRIS_DECODE_KERNEL=valu; measured against the MFMA tile).
+template <int D, int KVW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void int4_decode_valu_kernel(DecodeArgs a) {
+    decode_body<D, KVW, true>(a);
+}
+
 // Blocks of 16 query heads per kv head (more than one only for Hq / Hkv > 16,
 // each a workgroup of its own over the same pages).
 static int query_blocks(int g) { return g > 16 ? (g + 15) / 16 : 1; }
@@ -868,20 +1239,23 @@ static int pick_kvw(int g, int hkv, int64_t batch, int64_t max_pages, int64_t he
 
 // Dynamic LDS of one workgroup; above 64 KiB the kernel must be allowed to
 // use it (gfx950 has 160 KiB per CU): -1 if that fails.
-template <int D, int KVW>
+template <int D, int KVW, bool VALU>
 static int lds_bytes(int nw) {
     const int bytes = DecodeLayout<D, KVW>::WAVE_LDS * nw;
     static std::atomic<uint64_t> lds_raised{0};
-    if (bytes > 65536 && allow_full_lds(reinterpret_cast<const void*>(&int4_decode_kernel<D, KVW>), lds_raised) != kOk)
-        return -1;
+    const void* k;
+    if constexpr (VALU) k = reinterpret_cast<const void*>(&int4_decode_valu_kernel<D, KVW>);
+    else k = reinterpret_cast<const void*>(&int4_decode_kernel<D, KVW>);
+    if (bytes > 65536 && allow_full_lds(k, lds_raised) != kOk) return -1;
     return bytes;
 }
 
-template <int D, int KVW>
+template <int D, int KVW, bool VALU = false>
 static int launch_decode(dim3 grid, dim3 block, int nw, hipStream_t s, const DecodeArgs& a) {
-    const int lds = lds_bytes<D, KVW>(nw);
+    const int lds = lds_bytes<D, KVW, VALU>(nw);
     if (lds < 0) return kLaunchError;
-    hipLaunchKernelGGL((int4_decode_kernel<D, KVW>), grid, block, lds, s, a);
+    if constexpr (VALU) hipLaunchKernelGGL((int4_decode_valu_kernel<D, KVW>), grid, block, lds, s, a);
+    else hipLaunchKernelGGL((int4_decode_kernel<D, KVW>), grid, block, lds, s, a);
     return kOk;
 }
 
@@ -903,15 +1277,21 @@ constexpr int64_t kPagesMinBytes = 100000000;  // K/V bytes above which the page
 // so the plan's waves_per_block names the kernel for the launch.  A plan
 // asked for 16 waves uses the page kernel wherever it supports the shape;
 // asked for 1-4, or with IRIS_DECODE_KERNEL=general in the environment (A/B
-// measurements), the general kernel.  Left to choose, the plan takes the page
+// measurements), the general kernel; IRIS_DECODE_KERNEL=valu runs the general
+// kernel with its VALU tile instead of MFMA (g = 4 at D = 128, g = 16 at
+// D = 64; other shapes are refused).  Left to choose, the plan takes the page
 // kernel where it is the faster one: head_dim 128 with at most 4 query heads
 // per kv head and at least 4 kv heads (8 KB page slabs, the GQA shapes of
 // 7-70B models), over batches of similar lengths (its one workgroup per CU
 // balances ragged batches worse than the general kernel's many small ones)
 // that read at least kPagesMinBytes of K/V.
+static bool valu_selected() {
+    const char* sel = getenv("IRIS_DECODE_KERNEL");
+    return sel != nullptr && strcmp(sel, "valu") == 0;
+}
 static bool pages_allowed(int32_t waves_per_block) {
     const char* sel = getenv("IRIS_DECODE_KERNEL");
-    if (sel != nullptr && strcmp(sel, "general") == 0) return false;
+    if (sel != nullptr && (strcmp(sel, "general") == 0 || strcmp(sel, "valu") == 0)) return false;
     return waves_per_block <= 0 || waves_per_block == pages_waves();
 }
 static bool pages_preferred(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
@@ -1072,7 +1452,13 @@ extern "C" int iris_int4_paged_decode_attention(
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid((unsigned)nblocks), block(64 * waves_per_block);
     int st;
-    if (head_dim == 128) {
+    if (valu_selected()) {
+        // The VALU tile covers the two layouts with 16 columns of one or four
+        // kv heads: g = 4 at D = 128 (KVW 4) and g = 16 at D = 64 (KVW 1).
+        if (head_dim == 128 && kvw == 4 && g == 4) st = launch_decode<128, 4, true>(grid, block, waves_per_block, s, a);
+        else if (head_dim == 64 && kvw == 1 && g == 16) st = launch_decode<64, 1, true>(grid, block, waves_per_block, s, a);
+        else return kInvalidArgument;
+    } else if (head_dim == 128) {
         if (kvw == 4) st = launch_decode<128, 4>(grid, block, waves_per_block, s, a);
         else if (kvw == 2) st = launch_decode<128, 2>(grid, block, waves_per_block, s, a);
         else st = launch_decode<128, 1>(grid, block, waves_per_block, s, a);

@@ -158,41 +158,6 @@ __device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t 
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Maximum / sum over the 16 lanes of a row (DPP: xor 1, xor 2, then the
-// half-row and row mirrors).
-__device__ __forceinline__ float dpp_f(float x, int ctrl) {
-    switch (ctrl) {
-        case 0: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true));
-        case 1: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true));
-        case 2: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xF, 0xF, true));
-        default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xF, 0xF, true));
-    }
-}
-// Row maximum as four fused DPP maxima (v_max_f32_dpp; a VGPR a VALU
-// instruction wrote is read through DPP two wait states later).  NaN
-// operands follow v_max_f32: the other operand is returned.
-__device__ __forceinline__ float row16_max(float x) {
-    float y;
-    asm volatile(
-        "s_nop 1\n\t"
-        "v_max_f32_dpp %0, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
-        "s_nop 1\n\t"
-        "v_max_f32_dpp %0, %0, %0 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
-        "s_nop 1\n\t"
-        "v_max_f32_dpp %0, %0, %0 row_half_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
-        "s_nop 1\n\t"
-        "v_max_f32_dpp %0, %0, %0 row_mirror row_mask:0xf bank_mask:0xf bound_ctrl:1"
-        : "=&v"(y)
-        : "v"(x));
-    return y;
-}
-__device__ __forceinline__ float row16_sum(float x) {
-    x += dpp_f(x, 0);
-    x += dpp_f(x, 1);
-    x += dpp_f(x, 2);
-    return x + dpp_f(x, 3);
-}
-
 // Consecutive logical workgroup ids (the chunks of one sequence) on one XCD.
 __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
     constexpr int kXcds = 8;

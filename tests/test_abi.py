@@ -246,6 +246,27 @@ def test_decode_kernel_environment_switch(monkeypatch):
     assert decode_plan(*shape, waves_per_block=16)[2] == 4
 
 
+def test_valu_tile_switch_covers_two_layouts(monkeypatch):
+    # IRIS_DECODE_KERNEL=valu plans the general kernel and runs its VALU tile
+    # for g = 4 at D = 128 (four kv heads a wave) and g = 16 at D = 64; every
+    # other shape is refused before any HIP call (null pointers are safe).
+    shape = (32, 32, 8, 128, 256, 32 * 4096, 4096)
+    monkeypatch.setenv("IRIS_DECODE_KERNEL", "valu")
+    assert decode_plan(*shape)[2] == 4
+    assert decode_plan(*shape, waves_per_block=16)[2] == 4
+    lib = _lib.lib()
+    null = None
+    def call(B, Hq, Hkv, D, maxP):
+        return lib.iris_int4_paged_decode_attention(null, null, null, null, null, null, null, null, 0,
+                                                    null, 0, B, Hq, Hkv, D, 16, 8, maxP, ctypes.c_float(0.1),
+                                                    64, (maxP + 127) // 128, 4, null)
+    assert call(2, 8, 2, 64, 4) == 1       # g = 4 at D = 64
+    assert call(2, 8, 2, 128, 4) == 1      # g = 4 at D = 128, but two kv heads a wave
+    assert call(2, 16, 2, 128, 4) == 1     # g = 8
+    assert call(2, 16, 1, 256, 4) == 1     # D = 256
+    assert call(2, 16, 4, 128, 4) == 1     # g = 4, Hkv = 4: one kv head a wave at this size
+
+
 def test_fused_api_requires_a_gpu_when_none_is_present():
     import torch
 

@@ -449,3 +449,70 @@ def test_wider_scope_matches_eager(device, kernel, hq, hkv, d, page, lens, tps):
                                       waves_per_block=KERNELS[kernel])
     torch.cuda.synchronize(device)
     assert_attention_close(out, want, f"Hq={hq} Hkv={hkv} D={d} P={page}")
+
+
+# ------------------------------------------------------------------ VALU tile
+# IRIS_DECODE_KERNEL=valu: the general kernel with v_dot2c chains (DPP row
+# broadcasts) in place of its MFMAs -- the alternative the MFMA tile is
+# measured against -- held to the same contract on the layouts it covers
+# (g = 4 at D = 128 with four kv heads a wave, g = 16 at D = 64).
+@pytest.mark.parametrize("cfg", [2, 3, 4])
+def test_valu_tile_matches_eager(device, cfg, monkeypatch):
+    monkeypatch.setenv("IRIS_DECODE_KERNEL", "valu")
+    case, cpu, gpu = prepared(cfg, device)
+    if cfg not in _WANT:
+        log(f"decode: config {cfg} checker")
+        _WANT[cfg] = eager_fp32(case, cpu)
+    want32 = _WANT[cfg]
+    got32 = run(case, gpu, device, torch.float32, waves_per_block=4)
+    e32 = assert_attention_close(got32, want32, f"cfg{cfg} valu fp32")
+    got16 = run(case, gpu, device, waves_per_block=4)
+    e16 = assert_attention_close(got16, want32.to(torch.float16), f"cfg{cfg} valu fp16")
+    log(f"decode: config {cfg} valu max-abs err fp32 {e32:.2e} fp16 {e16:.2e}")
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 1, 64)])
+@pytest.mark.parametrize("tps", [0, 96, 1024])
+def test_valu_tile_ragged_and_split(device, monkeypatch, hq, hkv, d, tps):
+    # Lengths with partial pages and partial 32-token tiles (1, 17, 33), a
+    # full table row and one token short of it; one chunk, 3-tile chunks
+    # (43 a sequence) and 32-tile chunks.
+    monkeypatch.setenv("IRIS_DECODE_KERNEL", "valu")
+    lens = [1, 17, 33, 1000, 4095, 4096]
+    log(f"decode valu: Hq={hq} Hkv={hkv} D={d} lens={lens} split={tps}")
+    g = torch.Generator().manual_seed(hq + d + tps)
+    B, max_pages = len(lens), 257
+    num_pages = B * max_pages + 2
+    kd, vd, ks, vs = _quantized_pool(num_pages, 16, hkv, d, g)
+    bt = torch.randperm(num_pages, generator=g)[: B * max_pages].view(B, max_pages).to(torch.int32)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(torch.float16)
+    want = torch_eager_int4_paged_decode_attention(q, kd, vd, ks, vs, bt, sl, out_dtype=torch.float32)
+    qg, btg, slg = to(device, q, bt, sl)
+    cache = to(device, kd, vd, ks, vs)
+    out = torch.empty(q.shape, dtype=torch.float32, device=device)
+    fused_int4_paged_decode_attention(qg, *cache, btg, slg, out, tokens_per_split=tps, waves_per_block=4)
+    torch.cuda.synchronize(device)
+    assert_attention_close(out, want, f"valu Hq={hq} Hkv={hkv} D={d} split={tps}")
+
+
+def test_valu_tile_nan_poisoned_tails(device, monkeypatch):
+    # As test_nan_poisoned_tails_do_not_leak, on the VALU tile.
+    monkeypatch.setenv("IRIS_DECODE_KERNEL", "valu")
+    case, cpu, gpu = prepared(3, device)
+    clean = run(case, gpu, device, torch.float32, waves_per_block=4)
+    kd, vd, ks, vs = (t.clone() for t in cpu)
+    g = torch.Generator().manual_seed(98)
+    for b in range(case.config.batch):
+        n = int(case.seq_lens[b])
+        last = int(case.block_table[b, (n - 1) // 16])
+        tail = slice(n % 16 if n % 16 else 16, 16)
+        ks[last, tail] = float("nan")
+        vs[last, tail] = float("nan")
+        kd[last, tail] = torch.randint(0, 256, kd[last, tail].shape, dtype=torch.uint8, generator=g)
+        vd[last, tail] = torch.randint(0, 256, vd[last, tail].shape, dtype=torch.uint8, generator=g)
+    ks[case.pad_page] = float("nan")
+    vs[case.pad_page] = float("inf")
+    poisoned = run(case, to(device, kd, vd, ks, vs), device, torch.float32, waves_per_block=4)
+    assert torch.isfinite(poisoned).all()
+    assert torch.equal(poisoned, clean)
