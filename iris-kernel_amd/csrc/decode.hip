@@ -151,10 +151,10 @@ __device__ __forceinline__ void swap16(uint32_t& a, uint32_t& b) {
 __device__ __forceinline__ float row_max4(float x) {
     uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
     swap32(a, b);  // a = low half on both halves, b = high half on both halves
-    uint32_t c = __builtin_bit_cast(uint32_t, fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b)));
+    uint32_t c = __builtin_bit_cast(uint32_t, __builtin_elementwise_maximum(as_f32(a), as_f32(b)));
     uint32_t d = c;
     swap16(c, d);  // c = even rows on both rows of a pair, d = odd rows
-    return fmaxf(__builtin_bit_cast(float, c), __builtin_bit_cast(float, d));
+    return __builtin_elementwise_maximum(as_f32(c), as_f32(d));
 }
 
 __device__ __forceinline__ float row_sum4(float x) {
@@ -325,15 +325,6 @@ __device__ __forceinline__ void wait_vmem_all() {
 __device__ __forceinline__ uint32_t opaque(uint32_t x) {
     asm volatile("" : "+v"(x));
     return x;
-}
-
-// A wave-uniform pointer materialised in SGPRs: a per-lane choice between
-// two such pointers then stays a choice between two computed addresses (the
-// compiler would otherwise choose between the page ids and multiply per lane).
-__device__ __forceinline__ const uint8_t* sgpr_ptr(const uint8_t* p) {
-    uint64_t v = (uint64_t)(uintptr_t)p;
-    asm volatile("" : "+s"(v));
-    return reinterpret_cast<const uint8_t*>(v);
 }
 
 // Buffer resource over one page of a cache tensor (raw, stride 0, 32-bit
@@ -536,6 +527,17 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
         const int tau = qi / SW, w = qi % SW;
         s_loff[it] = (uint32_t)((((tau & 15) * hkv + kv0) * G + 2 * w) * 2);
     }
+    // The same as addresses from the tensor bases: a load's lane address is
+    // then (the lane's page) * (page bytes) + base, one v_mad_u64_u32 with
+    // no per-page 64-bit scalar arithmetic.
+    uint64_t v_lbase[1], ks_lbase[2], vs_lbase[2];
+#pragma unroll
+    for (int it = 0; it < L::NVO; ++it) v_lbase[it] = (uint64_t)(uintptr_t)a.v_data + v_loff[it];
+#pragma unroll
+    for (int it = 0; it < L::NSO; ++it) {
+        ks_lbase[it] = (uint64_t)(uintptr_t)a.k_scale + s_loff[it];
+        vs_lbase[it] = (uint64_t)(uintptr_t)a.v_scale + s_loff[it];
+    }
     // tr8 reads: supplier row s = n reads token tau(jq, k = n >> 1), half
     // n & 1; the chunk of (kv j, group grp) sits at position (j G + grp) ^ f.
     const int trk = n >> 1;
@@ -548,21 +550,25 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     uint8_t* const stage = smem + wave * L::WAVE_LDS;
 
     // ---- loads of one tile: K codes into registers `kw` ...
+    // (Lane address = page id * page bytes + this lane's address from the
+    // tensor base: one v_mad_u64_u32 per page, the per-load constants in the
+    // loads' offset fields.)
+    const uint64_t k_lbase = (uint64_t)(uintptr_t)a.k_data + k_off;
     auto issue_k = [&](int tile, uint32_t (&kw)[2][L::KREGS]) {
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-            const auto rs = page_rsrc(a.k_data + page_of(2 * tile + r) * page_data, (uint32_t)page_data);
-            const uint32_t ko = opaque(k_off);
+            const uint8_t* const kp = reinterpret_cast<const uint8_t*>(
+                (uint64_t)(uint32_t)page_of(2 * tile + r) * (uint32_t)page_data + k_lbase);
 #pragma unroll
             for (int j = 0; j < KVW; ++j) {
                 if constexpr (D == 128) {
-                    const u32x4_t x = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, ko + j * HB, 0, kStreamAux));
+                    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(kp + j * HB);
 #pragma unroll
                     for (int q = 0; q < 4; ++q) kw[r][j * G + q] = x[q];
                 } else {
 #pragma unroll
                     for (int grp = 0; grp < G; ++grp)
-                        kw[r][j * G + grp] = __builtin_amdgcn_raw_buffer_load_b32(rs, ko + (j * HB + grp * 16), 0, kStreamAux);
+                        kw[r][j * G + grp] = *reinterpret_cast<const uint32_t*>(kp + j * HB + grp * 16);
                 }
             }
         }
@@ -582,15 +588,15 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
                                                          (tau0 & 15) * hkv * HB, 0, kStreamAux);
             }
         } else {
-            // lanes of both pages in one load: the page base (uniform) picked
-            // per lane, plus the lane's offset inside the page
-            const uint8_t* const vpb[2] = {sgpr_ptr(a.v_data + pg[0] * page_data),
-                                           sgpr_ptr(a.v_data + pg[1] * page_data)};
+            // lanes of both pages in one load: the lane's page id (one of the
+            // two, uniform) times the page size, plus its address from the base
+            const uint32_t p0 = (uint32_t)pg[0], p1 = (uint32_t)pg[1];
 #pragma unroll
             for (int it = 0; it < L::NV; ++it) {
                 const int tau = (it * 64 + lane) / C;
-                __builtin_amdgcn_global_load_lds(((tau >> 4) ? vpb[1] : vpb[0]) + v_loff[it],
-                                                 (IRIS_LDS void*)(vb + it * 1024), 16, 0, kStreamAux);
+                const uint64_t ad = (uint64_t)((tau >> 4) ? p1 : p0) * (uint32_t)page_data + v_lbase[it];
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(ad), (IRIS_LDS void*)(vb + it * 1024),
+                                                 16, 0, kStreamAux);
             }
         }
         if constexpr (STPI <= 16) {
@@ -610,18 +616,15 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
                                                          s_lane, soff, 0, kStreamAux);
             }
         } else {
-            const uint8_t* const ksb = reinterpret_cast<const uint8_t*>(a.k_scale);
-            const uint8_t* const vsb = reinterpret_cast<const uint8_t*>(a.v_scale);
-            const uint8_t* const kpb[2] = {sgpr_ptr(ksb + pg[0] * page_scale), sgpr_ptr(ksb + pg[1] * page_scale)};
-            const uint8_t* const spb[2] = {sgpr_ptr(vsb + pg[0] * page_scale), sgpr_ptr(vsb + pg[1] * page_scale)};
+            const uint32_t p0 = (uint32_t)pg[0], p1 = (uint32_t)pg[1];
 #pragma unroll
             for (int it = 0; it < L::NS; ++it) {
                 const int qi = it * 64 + lane;
                 if (L::SDW % 64 == 0 || qi < L::SDW) {
-                    const int hi = (qi / SW) >> 4;
-                    __builtin_amdgcn_global_load_lds((hi ? kpb[1] : kpb[0]) + s_loff[it],
+                    const uint64_t po = (uint64_t)(((qi / SW) >> 4) ? p1 : p0) * (uint32_t)page_scale;
+                    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(po + ks_lbase[it]),
                                                      (IRIS_LDS void*)(vb + L::VBUF + it * 256), 4, 0, kStreamAux);
-                    __builtin_amdgcn_global_load_lds((hi ? spb[1] : spb[0]) + s_loff[it],
+                    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(po + vs_lbase[it]),
                                                      (IRIS_LDS void*)(vb + L::VBUF + L::SBUF + it * 256), 4, 0, kStreamAux);
                 }
             }
@@ -757,16 +760,22 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
             }
         }
         if (next < t_end) issue_k(next, kw);
-        // ---- online softmax (base 2, lazy rescale)
+        // ---- online softmax (base 2, lazy rescale).  Token 16 r + 4 jq + i
+        // of the tile is valid iff 16 r + i < nval.  (Maxima as
+        // __builtin_elementwise_maximum: v_maximum3, which needs no
+        // canonicalised operands after the masking selects; the scores are
+        // finite or -inf.)
+        const int nval = seq_len - tok_base - 4 * jq;
         if (!full) {
 #pragma unroll
             for (int r = 0; r < 2; ++r)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    if (tok_base + 16 * r + 4 * jq + i >= seq_len) s[r][i] = -INFINITY;
+                    if (16 * r + i >= nval) s[r][i] = -INFINITY;
         }
-        float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
-                         fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+        auto vmax = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
+        float mx = vmax(vmax(vmax(s[0][0], s[0][1]), vmax(s[0][2], s[0][3])),
+                        vmax(vmax(s[1][0], s[1][1]), vmax(s[1][2], s[1][3])));
         mx = row_max4(mx);  // finite: token tile*32 < seq_len
         if (__ballot(mx > m_run + lazy) != 0) {
             const float m_new = fmaxf(m_run, mx);
@@ -791,14 +800,17 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
                 p[r][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r][i], c24, moff));
                 l_part += p[r][i];
             }
-        // ---- PV
-        half_t vsv[2][4][G];
+        // ---- PV.  V scales as dwords (groups 2h, 2h + 1 of a token), so a
+        // masked token clears whole dwords and each half feeds its product
+        // directly.
+        uint32_t vsd[2][4][G / 2];
+        const uint32_t* const vs_w = reinterpret_cast<const uint32_t*>(vs_lds);
 #pragma unroll
         for (int r = 0; r < 2; ++r)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int grp = 0; grp < G; ++grp) vsv[r][i][grp] = vs_lds[(16 * r + i) * KVW * G + grp];
+                for (int h = 0; h < G / 2; ++h) vsd[r][i][h] = vs_w[(16 * r + i) * KVW * G / 2 + h];
         if (!full) {
             // Tokens past seq_len may hold any bytes: never let their scale
             // reach the product (0 * NaN).  A real branch: the asm keeps the
@@ -808,9 +820,9 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
             for (int r = 0; r < 2; ++r)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    if (tok_base + 16 * r + 4 * jq + i >= seq_len) {
+                    if (16 * r + i >= nval) {
 #pragma unroll
-                        for (int grp = 0; grp < G; ++grp) vsv[r][i][grp] = (half_t)0.0f;
+                        for (int h = 0; h < G / 2; ++h) vsd[r][i][h] = 0u;
                     }
         }
         // V operands: the chunk of (kv j, group grp) sits at tr_base ^
@@ -837,7 +849,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
 #pragma unroll
             for (int sl = 0; sl < 8; ++sl) {
                 const int r = kVSlotByte[sl] >> 2, i = kVSlotByte[sl] & 3;
-                bp[sl] = (half_t)__builtin_fmaf(p[r][i], (float)vsv[r][i][grp], 0.0f);
+                bp[sl] = (half_t)__builtin_fmaf(p[r][i], (float)as_half2(vsd[r][i][grp >> 1])[grp & 1], 0.0f);
             }
             const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
 #pragma unroll
