@@ -80,6 +80,7 @@ constexpr int kStreamAux = IRIS_STREAM_AUX;
 
 typedef int int2v_t __attribute__((ext_vector_type(2)));
 #define IRIS_LDS __attribute__((address_space(3)))
+#define IRIS_GLOBAL __attribute__((address_space(1)))
 
 struct DecodeArgs {
     const half_t* q;
@@ -470,6 +471,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
 
     // Physical page of logical page lp (clamped to the sequence's last page;
     // tokens past seq_len are masked).  p0 <= lp' < p0 + 2 * chunk_tiles.
+    // Call it in uniform control flow only: the lane it reads belongs to a
+    // VGPR select, which lanes masked off by a divergent branch leave stale.
     auto page_of = [&](int lp) -> int64_t {
         const int rel = min(lp, last_lp) - p0;
         return (int64_t)__builtin_amdgcn_readlane(rel < 64 ? pid0 : pid1, rel & 63);
@@ -554,21 +557,42 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     // tensor base: one v_mad_u64_u32 per page, the per-load constants in the
     // loads' offset fields.)
     const uint64_t k_lbase = (uint64_t)(uintptr_t)a.k_data + k_off;
+    // D = 64, one kv head a wave: one 16-byte load a lane covers the tile.
+    // Lane (n, jq) reads row n of page jq >> 1, bytes 16 (jq & 1) .. + 15
+    // (group jq & 1); a 4 x 4 transpose across the rows at use turns that
+    // into dword jq of every (page, group), the MFMA A layout.
+    const uint64_t k64_lbase = (uint64_t)(uintptr_t)a.k_data + (uint32_t)(n * hkv + kv0) * HB + 16 * (jq & 1);
     auto issue_k = [&](int tile, uint32_t (&kw)[2][L::KREGS]) {
+        if constexpr (D == 64 && KVW == 1) {
+            // (both page ids first, in uniform control flow: page_of reads a
+            // lane of a VGPR select, which a divergent branch would leave
+            // unwritten in its inactive lanes)
+            const uint32_t pa = (uint32_t)page_of(2 * tile), pb = (uint32_t)page_of(2 * tile + 1);
+            const uint32_t pk = (jq >> 1) ? pb : pa;
+            const u32x4_t x =
+                *reinterpret_cast<const IRIS_GLOBAL u32x4_t*>((uint64_t)pk * (uint32_t)page_data + k64_lbase);
+            kw[0][0] = x[0];
+            kw[0][1] = x[1];
+            kw[1][0] = x[2];
+            kw[1][1] = x[3];
+            return;
+        }
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
-            const uint8_t* const kp = reinterpret_cast<const uint8_t*>(
+            // (a global-address-space pointer: global_load, not flat_load, whose
+            // pending count would also hold back the tile's LDS reads)
+            const IRIS_GLOBAL uint8_t* const kp = reinterpret_cast<const IRIS_GLOBAL uint8_t*>(
                 (uint64_t)(uint32_t)page_of(2 * tile + r) * (uint32_t)page_data + k_lbase);
 #pragma unroll
             for (int j = 0; j < KVW; ++j) {
                 if constexpr (D == 128) {
-                    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(kp + j * HB);
+                    const u32x4_t x = *reinterpret_cast<const IRIS_GLOBAL u32x4_t*>(kp + j * HB);
 #pragma unroll
                     for (int q = 0; q < 4; ++q) kw[r][j * G + q] = x[q];
                 } else {
 #pragma unroll
                     for (int grp = 0; grp < G; ++grp)
-                        kw[r][j * G + grp] = *reinterpret_cast<const uint32_t*>(kp + j * HB + grp * 16);
+                        kw[r][j * G + grp] = *reinterpret_cast<const IRIS_GLOBAL uint32_t*>(kp + j * HB + grp * 16);
                 }
             }
         }
@@ -614,6 +638,17 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
                                                          soff, 0, kStreamAux);
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(vr[r], (IRIS_LDS void*)(vb + L::VBUF + L::SBUF + it * 256), 4,
                                                          s_lane, soff, 0, kStreamAux);
+            }
+        } else if (D == 64 && KVW == 1 && hkv == 1) {
+            // One kv head in the cache: a page's scales of one tensor are 64
+            // contiguous bytes, so lanes 0-15 bring both tensors of both pages
+            // in one 16-byte-a-lane load (lane l: tensor l >> 3, page
+            // (l >> 2) & 1, piece l & 3), landing as the two scale blocks.
+            if (lane < 16) {
+                const uint64_t pb = (uint64_t)(uint32_t)(((lane >> 2) & 1) ? pg[1] : pg[0]) * (uint32_t)page_scale;
+                const uint64_t tb = (uint64_t)(uintptr_t)((lane >> 3) ? (const void*)a.v_scale : (const void*)a.k_scale);
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(tb + pb + 16 * (lane & 3)),
+                                                 (IRIS_LDS void*)(vb + L::VBUF), 16, 0, kStreamAux);
             }
         } else {
             const uint32_t p0 = (uint32_t)pg[0], p1 = (uint32_t)pg[1];
@@ -742,6 +777,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
 #pragma unroll
                     for (int q = 0; q < 4; ++q) kw[r][j * G + q] = x[q];
                 }
+        } else if constexpr (D == 64 && KVW == 1) {
+            u32x4_t x = {kw[0][0], kw[0][1], kw[1][0], kw[1][1]};
+            transpose_rows4(x);
+            kw[0][0] = x[0];
+            kw[0][1] = x[1];
+            kw[1][0] = x[2];
+            kw[1][1] = x[3];
         }
         // ---- QK: s[r][i] is token 16r + 4jq + i, column n (MFMA units)
         float s[2][4];
@@ -902,6 +944,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
 #pragma unroll
                     for (int q = 0; q < 4; ++q) kw[r][j * G + q] = x[q];
                 }
+        } else if constexpr (D == 64 && KVW == 1) {
+            u32x4_t x = {kw[0][0], kw[0][1], kw[1][0], kw[1][1]};
+            transpose_rows4(x);
+            kw[0][0] = x[0];
+            kw[0][1] = x[1];
+            kw[1][0] = x[2];
+            kw[1][1] = x[3];
         }
         // ---- QK per 16-token half: partial sums over this row's chunk,
         // scaled per (token, group), then the four rows' partial sums added:
