@@ -48,18 +48,41 @@ __device__ __forceinline__ uint32_t next_quad(uint32_t x) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x104, 0xF, 0xF, true);
 }
 
+// Partner chunk's word for the chunk-aligned RoPE: with ROR8 (16 lanes a
+// row, rotary_dim 128) chunk c pairs with c ^ 8, one DPP row rotate by 8;
+// otherwise a lane shuffle to `partner`.
+template <bool ROR8>
+__device__ __forceinline__ uint32_t rope_partner(uint32_t x, int partner) {
+    if constexpr (ROR8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, false);
+    else return (uint32_t)__shfl((int)x, partner, 64);
+}
+
+// Maximum over the 4 lanes of a quad (one 32-dim group): DPP quad swaps,
+// NaN-propagating maxima.
+__device__ __forceinline__ half2_t quad_amax(half2_t m) {
+    m = amax_max(m, as_half2((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(m), 0xB1, 0xF, 0xF, false)));
+    return amax_max(m, as_half2((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(m), 0x4E, 0xF, 0xF, false)));
+}
+
 // RPT rows per thread: rows k * kRowsPerBlock + (thread's row) of the
-// block's RPT * kRowsPerBlock, every load of all RPT rows issued before the
-// first use (the slot, position, K and V loads together, then the RoPE rows),
-// so a wave keeps RPT rows of loads in flight.  Large appends use RPT = 2.
-template <int ROWLANES, int RPT, bool PER_ELEM>
+// block's RPT * kRowsPerBlock.  Loads go out in three waves, each for all RPT
+// rows: the slot and position words, then the K and V chunks, then (once the
+// positions are in) the RoPE table chunks, so the table reads overlap the
+// K/V reads instead of following them.  Large appends use RPT = 2.
+//
+// Row r is (token r / n_heads, head r % n_heads); the quotient is taken as
+// trunc((r + 0.5) * RN64(1 / n_heads)) in fp64, exact for r < 2^31 and
+// n_heads < 2^20 (the error, below 2^-21, stays under the 0.5 / n_heads
+// margin).  The cache row of (slot, head) is slot * n_heads + head: pages
+// are page_size consecutive slots, so the page split cancels.
+template <int ROWLANES, int RPT, bool PER_ELEM, bool ROR8>
 __global__ __launch_bounds__(256) void rope_int4_paged_append_kernel(
     const u32x4_t* __restrict__ key, const u32x4_t* __restrict__ value,
     const int32_t* __restrict__ positions, const int32_t* __restrict__ slot_mapping,
     const half_t* __restrict__ cos_cache, const half_t* __restrict__ sin_cache,
-    uint32_t* __restrict__ k_data, uint32_t* __restrict__ v_data,
-    half_t* __restrict__ k_scale, half_t* __restrict__ v_scale,
-    int64_t n_rows, int n_heads, int head_dim, int rotary_dim, int page_size) {
+    u32x4_t* __restrict__ k_data, u32x4_t* __restrict__ v_data,
+    uint32_t* __restrict__ k_scale, uint32_t* __restrict__ v_scale,
+    int n_rows, int n_heads, double inv_heads, int head_dim, int rotary_dim) {
     constexpr int kRowsPerBlock = 256 / ROWLANES;
     const int chunks = head_dim >> 3;  // 8 dims per lane
     const int lane = threadIdx.x & 63;
@@ -71,58 +94,68 @@ __global__ __launch_bounds__(256) void rope_int4_paged_append_kernel(
     const int rot_c = rotary_dim >> 3, half_c = rotary_dim >> 4;
     const bool rotated = !PER_ELEM && c < rot_c;
     const bool lo_half = c < half_c;
-    const int cc = lo_half ? c : c - half_c;
+    const int cc = rotated ? (lo_half ? c : c - half_c) : 0;
     const int partner = (lane - c_raw) + (lo_half ? c + half_c : (rotated ? c - half_c : c));
+    // x' * sin enters the lower rotary half negated: RN16(x' * -sin) is
+    // -RN16(x' * sin), and a + (-b) is a - b.
+    const uint32_t sin_sign = lo_half ? 0x80008000u : 0u;
 
-    int64_t rr[RPT];
+    int row[RPT], head[RPT], tok[RPT];
     bool live[RPT];
-    int slot[RPT], pos[RPT], head[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const uint32_t r = blockIdx.x * (uint32_t)(kRowsPerBlock * RPT) + k * kRowsPerBlock + threadIdx.x / ROWLANES;
+        live[k] = r < (uint32_t)n_rows && c_raw < chunks;
+        row[k] = r < (uint32_t)n_rows ? (int)r : 0;  // tail rows mirror row 0, store nothing
+        tok[k] = (int)(((double)row[k] + 0.5) * inv_heads);
+        head[k] = row[k] - tok[k] * n_heads;
+    }
+    int slot[RPT], pos[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        slot[k] = slot_mapping[tok[k]];
+        pos[k] = positions[tok[k]];
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep the three load waves in this order
     u32x4_t kx[RPT], vx[RPT];
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
-        const int64_t row = (int64_t)blockIdx.x * (kRowsPerBlock * RPT) + k * kRowsPerBlock + threadIdx.x / ROWLANES;
-        live[k] = row < n_rows && c_raw < chunks;
-        rr[k] = row < n_rows ? row : 0;  // tail rows mirror row 0, store nothing
-        const int64_t tok = rr[k] / n_heads;
-        head[k] = (int)(rr[k] - tok * n_heads);
-        slot[k] = slot_mapping[tok];
-        pos[k] = positions[tok];
-        kx[k] = key[rr[k] * chunks + c];
-        vx[k] = value[rr[k] * chunks + c];
+        kx[k] = key[(uint64_t)(uint32_t)row[k] * (uint32_t)chunks + c];
+        vx[k] = value[(uint64_t)(uint32_t)row[k] * (uint32_t)chunks + c];
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // Unconditional table loads (no branch for the compiler to sink the
+    // position loads into): with rotary_dim 0 the host points cos_cache and
+    // sin_cache at the key tensor and every lane reads its first 16 bytes.
     u32x4_t cx[RPT], sx[RPT];
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
         cx[k] = sx[k] = u32x4_t{0, 0, 0, 0};
-        // Positions of skipped tokens are not validated by the caller; read
-        // the RoPE table at row 0 for them (the result is discarded).
-        const int64_t p = slot[k] >= 0 ? pos[k] : 0;
-        if (rotated) {
+        if constexpr (!PER_ELEM) {
+            // Positions of skipped tokens are not validated by the caller;
+            // read the RoPE table at row 0 for them (the result is discarded).
+            const int64_t p = slot[k] >= 0 ? pos[k] : 0;
             cx[k] = *reinterpret_cast<const u32x4_t*>(cos_cache + p * hr + cc * 8);
             sx[k] = *reinterpret_cast<const u32x4_t*>(sin_cache + p * hr + cc * 8);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
-        u32x4_t kp;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) kp[q] = (uint32_t)__shfl((int)kx[k][q], partner, 64);
-
         half2_t kr[4], vr[4];
-        half2_t kmax2 = {0, 0}, vmax2 = {0, 0};
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            half2_t own = as_half2(kx[k][q]);
-            half2_t oth = as_half2(kp[q]);
-            half2_t a = own * as_half2(cx[k][q]);  // x*cos, rounded to fp16
-            half2_t b = oth * as_half2(sx[k][q]);  // x'*sin, rounded to fp16
-            kr[q] = rotated ? (lo_half ? a - b : a + b) : own;  // rounded to fp16
+            const half2_t own = as_half2(kx[k][q]);
+            const half2_t a = own * as_half2(cx[k][q]);                                    // x*cos, rounded to fp16
+            const half2_t b = as_half2(rope_partner<ROR8>(kx[k][q], partner)) *
+                              as_half2(sx[k][q] ^ sin_sign);                               // +-x'*sin, rounded
+            kr[q] = rotated ? a + b : own;                                                 // rounded to fp16
             vr[q] = as_half2(vx[k][q]);
         }
         if constexpr (PER_ELEM) {
             // Any even R: dim d < R takes its partner, cos and sin from memory.
-            const half_t* krow = reinterpret_cast<const half_t*>(key) + rr[k] * head_dim;
+            const half_t* krow = reinterpret_cast<const half_t*>(key) + (int64_t)row[k] * head_dim;
             const int64_t p = slot[k] >= 0 ? pos[k] : 0;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -140,21 +173,19 @@ __global__ __launch_bounds__(256) void rope_int4_paged_append_kernel(
                 }
             }
         }
+        // Group amax of K (low half) and V (high half) together: per-lane
+        // maxima of |x| over the even and the odd dims, then the quad.
+        half2_t km2 = __builtin_elementwise_abs(kr[0]), vm2 = __builtin_elementwise_abs(vr[0]);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            kmax2 = amax_max(kmax2, __builtin_elementwise_abs(kr[q]));
-            vmax2 = amax_max(vmax2, __builtin_elementwise_abs(vr[q]));
+        for (int q = 1; q < 4; ++q) {
+            km2 = amax_max(km2, __builtin_elementwise_abs(kr[q]));
+            vm2 = amax_max(vm2, __builtin_elementwise_abs(vr[q]));
         }
-        float kmax = amax_max((float)kmax2.x, (float)kmax2.y);
-        float vmax = amax_max((float)vmax2.x, (float)vmax2.y);
-        // Quad = one 32-dim group.
-        kmax = amax_max(kmax, __shfl_xor(kmax, 1, 64));
-        vmax = amax_max(vmax, __shfl_xor(vmax, 1, 64));
-        kmax = amax_max(kmax, __shfl_xor(kmax, 2, 64));
-        vmax = amax_max(vmax, __shfl_xor(vmax, 2, 64));
+        const half2_t kv_even = {km2.x, vm2.x}, kv_odd = {km2.y, vm2.y};
+        const half2_t kvmax = quad_amax(amax_max(kv_even, kv_odd));
 
-        const half_t ks16 = scale_from_amax(kmax);
-        const half_t vs16 = scale_from_amax(vmax);
+        const half_t ks16 = scale_from_amax((float)kvmax.x);
+        const half_t vs16 = scale_from_amax((float)kvmax.y);
         const uint32_t kword = pack_group8(kr, (float)ks16);
         const uint32_t vword = pack_group8(vr, (float)vs16);
 
@@ -168,15 +199,13 @@ __global__ __launch_bounds__(256) void rope_int4_paged_append_kernel(
         const uint32_t ks2 = (ks & 0xFFFFu) | (next_quad(ks) << 16);
         const uint32_t vs2 = (vs & 0xFFFFu) | (next_quad(vs) << 16);
         if (live[k] && slot[k] >= 0 && (c & 3) == 0) {
-            const int64_t page = slot[k] / page_size;
-            const int64_t off = slot[k] - page * page_size;
-            const int64_t cache_row = (page * page_size + off) * n_heads + head[k];
+            const uint64_t cache_row = (uint64_t)(uint32_t)slot[k] * (uint32_t)n_heads + (uint32_t)head[k];
             // D/2 bytes per row = chunks / 4 16-byte groups
-            reinterpret_cast<u32x4_t*>(k_data)[cache_row * (chunks >> 2) + (c >> 2)] = kq;
-            reinterpret_cast<u32x4_t*>(v_data)[cache_row * (chunks >> 2) + (c >> 2)] = vq;
+            k_data[cache_row * (uint32_t)(chunks >> 2) + (c >> 2)] = kq;
+            v_data[cache_row * (uint32_t)(chunks >> 2) + (c >> 2)] = vq;
             if ((c & 7) == 0) {  // D/32 scales per row, two per 32-bit word
-                reinterpret_cast<uint32_t*>(k_scale)[(cache_row * (head_dim >> 5) + (c >> 2)) >> 1] = ks2;
-                reinterpret_cast<uint32_t*>(v_scale)[(cache_row * (head_dim >> 5) + (c >> 2)) >> 1] = vs2;
+                k_scale[(cache_row * (uint32_t)(head_dim >> 5) + (c >> 2)) >> 1] = ks2;
+                v_scale[(cache_row * (uint32_t)(head_dim >> 5) + (c >> 2)) >> 1] = vs2;
             }
         }
     }
@@ -197,32 +226,41 @@ extern "C" int iris_rope_int4_paged_append(
         head_dim % 64 != 0 || head_dim > 512 || rotary_dim < 0 || rotary_dim > head_dim || rotary_dim % 2 != 0)
         return kInvalidArgument;
     if (num_tokens == 0) return kOk;
+    // 32-bit row indices and the fp64 row -> (token, head) split: a launch
+    // covers fewer than 2^31 rows (2^31 rows of even D = 64 are 256 GiB of
+    // fp16 K) of fewer than 2^20 heads.
+    if (num_kv_heads >= (1 << 20) || num_tokens > (((int64_t)1 << 31) - 1) / num_kv_heads) return kInvalidArgument;
     const int64_t n_rows = num_tokens * num_kv_heads;
     const int chunks = (int)(head_dim / 8);
     int rowlanes = 8;
     while (rowlanes < chunks) rowlanes <<= 1;
     const int64_t rows_per_block = 256 / rowlanes;
-    // Two rows a thread for large appends (MI355X, 4 x 8192 tokens, Hkv=8,
-    // D=128: 32.3 us against 32.8 with one and 33.8 with four); one for
-    // short appends, which are latency-bound either way.
+    // Two rows a thread for large appends, one for short appends, which are
+    // latency-bound either way.
     const int rpt = n_rows >= 65536 ? 2 : 1;
     const int64_t blocks = (n_rows + rows_per_block * rpt - 1) / (rows_per_block * rpt);
-    if (blocks > 0x7FFFFFFF) return kInvalidArgument;
     hipStream_t s = (hipStream_t)stream;
     const bool per_elem = rotary_dim % 16 != 0;
-#define IRIS_LAUNCH_APPEND(RL, RPT, PE)                                                                  \
-    hipLaunchKernelGGL((rope_int4_paged_append_kernel<RL, RPT, PE>), dim3((unsigned)blocks), dim3(256), 0, s, \
-                       (const u32x4_t*)key, (const u32x4_t*)value, positions, slot_mapping,              \
-                       (const half_t*)cos_cache, (const half_t*)sin_cache, (uint32_t*)k_data,            \
-                       (uint32_t*)v_data, (half_t*)k_scale, (half_t*)v_scale, n_rows,                    \
-                       (int)num_kv_heads, (int)head_dim, (int)rotary_dim, (int)page_size)
-#define IRIS_LAUNCH_APPEND_RPT(RL)                   \
-    if (per_elem) IRIS_LAUNCH_APPEND(RL, 1, true);   \
-    else if (rpt == 2) IRIS_LAUNCH_APPEND(RL, 2, false); \
-    else IRIS_LAUNCH_APPEND(RL, 1, false)
+    const bool ror8 = rowlanes == 16 && rotary_dim == 128;
+    const double inv_heads = 1.0 / (double)num_kv_heads;
+    if (rotary_dim == 0) cos_cache = sin_cache = key;  // a readable 16 bytes; the values are not used
+#define IRIS_LAUNCH_APPEND(RL, RPT, PE, ROR)                                                                   \
+    hipLaunchKernelGGL((rope_int4_paged_append_kernel<RL, RPT, PE, ROR>), dim3((unsigned)blocks), dim3(256), 0, s, \
+                       (const u32x4_t*)key, (const u32x4_t*)value, positions, slot_mapping,                     \
+                       (const half_t*)cos_cache, (const half_t*)sin_cache, (u32x4_t*)k_data,                    \
+                       (u32x4_t*)v_data, (uint32_t*)k_scale, (uint32_t*)v_scale, (int)n_rows,                   \
+                       (int)num_kv_heads, inv_heads, (int)head_dim, (int)rotary_dim)
+#define IRIS_LAUNCH_APPEND_RPT(RL)                          \
+    if (per_elem) IRIS_LAUNCH_APPEND(RL, 1, true, false);   \
+    else if (rpt == 2) IRIS_LAUNCH_APPEND(RL, 2, false, false); \
+    else IRIS_LAUNCH_APPEND(RL, 1, false, false)
     switch (rowlanes) {
         case 8: IRIS_LAUNCH_APPEND_RPT(8); break;
-        case 16: IRIS_LAUNCH_APPEND_RPT(16); break;
+        case 16:
+            if (ror8 && rpt == 2) IRIS_LAUNCH_APPEND(16, 2, false, true);
+            else if (ror8) IRIS_LAUNCH_APPEND(16, 1, false, true);
+            else IRIS_LAUNCH_APPEND_RPT(16);
+            break;
         case 32: IRIS_LAUNCH_APPEND_RPT(32); break;
         case 64: IRIS_LAUNCH_APPEND_RPT(64); break;
         default: return kInvalidArgument;

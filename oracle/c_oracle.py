@@ -37,8 +37,10 @@ def load() -> ctypes.CDLL:
         lib.ior_decode.restype = ctypes.c_int
         lib.ior_check_scale_mul.argtypes = []
         lib.ior_check_scale_mul.restype = _i64
-        lib.ior_check_quant_fast.argtypes = [ctypes.c_int, ctypes.c_int]
-        lib.ior_check_quant_fast.restype = _i64
+        lib.ior_check_quant_grid.argtypes = [ctypes.c_int, ctypes.c_int]
+        lib.ior_check_quant_grid.restype = _i64
+        lib.ior_check_pack_sum.argtypes = [ctypes.c_int32]
+        lib.ior_check_pack_sum.restype = _i64
         lib.ior_f32_to_f16_array.argtypes = [_p, _p, _i64]
         lib.ior_f16_to_f32_array.argtypes = [_p, _p, _i64]
         _lib = lib
@@ -120,5 +122,11 @@ def check_scale_mul() -> int:
     return int(load().ior_check_scale_mul())
 
 
-def check_quant_fast(rvariant: int, refine: bool = True) -> int:
-    return int(load().ior_check_quant_fast(int(rvariant), 1 if refine else 0))
+def check_quant_grid(rvariant: int, mode: int = 0) -> int:
+    """Mismatches of the kernels' two-rounding quantiser (ior_check_quant_grid)."""
+    return int(load().ior_check_quant_grid(int(rvariant), int(mode)))
+
+
+def check_pack_sum(bias_delta: int = 0) -> int:
+    """Mismatches of the kernels' shift-and-add nibble packing (ior_check_pack_sum)."""
+    return int(load().ior_check_pack_sum(int(bias_delta)))

@@ -302,20 +302,27 @@ int64_t ior_check_scale_mul(void) {
 }
 
 /*
- * Quantised value: the HIP append kernel computes, with r an approximation
- * of 1/s,
- *     y  = RN(x * r);  e = fma(-y, s, x);  y2 = fma(r, e, y)
- *     y2 = min(max(y2, -7), 7);  t = RN(y2 + 1.5 * 2^23)
- * and takes the low nibble of t's bit pattern as the two's-complement INT4
- * code.  Count the (x, s) pairs, over every scale s the quantiser can emit
- * (normal fp16 in [2^-14, RN16(65504/7)]) and every fp16 x with |x| <= 8 s,
- * where that nibble differs from the reference's clamp(rint(x / s)) & 0xF.
- * rvariant: 0 -> r = RN(1/s), -1 / +1 -> one float below / above it, which
- * covers any reciprocal accurate to 1 ulp.  refine = 0 drops the fma
- * correction (y2 = y); the tests use it to show that the check does detect
- * the round-half-even cases that a plain reciprocal multiply gets wrong.
+ * Quantised value: the HIP kernels compute, with r an approximation of 1/s
+ * (v_rcp_f32, accurate to 1 ulp),
+ *     t = RN(RN(x * r + 3072) + (1.5 * 2^23 - 3072))      (the first an fma)
+ * and take the low nibble of t's bit pattern as the two's-complement INT4
+ * code, with no clamp.  Count the (x, s) pairs where that nibble differs from
+ * the reference's clamp(rint(x / s), -7, 7) & 0xF, over every scale s the
+ * quantiser can emit (normal fp16 in [2^-14, RN16(65504/7)]) and every fp16 x
+ * that can be quantised with it: |x| at most the largest fp16 amax whose
+ * scale is s, since x belongs to the group whose amax set s.
+ * rvariant: r = RN(1/s) moved by rvariant floats (+-2 covers any reciprocal
+ * accurate to 2 ulp).  mode 1 widens x to |x| <= 8 s, past any group amax,
+ * where the missing clamp shows; mode 2 rounds in one step,
+ * t = RN(x * r + 1.5 * 2^23), which gets round-half-even cases wrong.  The
+ * tests use modes 1 and 2 to show that the check detects such mistakes.
  */
-int64_t ior_check_quant_fast(int rvariant, int refine) {
+int64_t ior_check_quant_grid(int rvariant, int mode) {
+    static float amax_top[0x10000];
+    for (uint32_t h = 0; h <= 0x7BFFu; ++h) { /* fp16 bit order is magnitude order */
+        const float a = ior_f16_to_f32((uint16_t)h);
+        amax_top[scale_ref(a)] = a;
+    }
     const uint16_t smax = scale_ref(65504.0f);
     int64_t bad = 0;
     int32_t sh;
@@ -323,23 +330,52 @@ int64_t ior_check_quant_fast(int rvariant, int refine) {
     for (sh = 0x0400; sh <= (int32_t)smax; ++sh) {
         const float s = ior_f16_to_f32((uint16_t)sh);
         float r = 1.0f / s;
-        if (rvariant < 0) r = nextafterf(r, 0.0f);
-        if (rvariant > 0) r = nextafterf(r, INFINITY);
-        const float lim = 8.0f * s;
+        for (int i = 0; i < abs(rvariant); ++i) r = nextafterf(r, rvariant < 0 ? 0.0f : INFINITY);
+        const float lim = mode == 1 ? 8.0f * s : amax_top[sh];
         for (uint32_t xh = 0; xh <= 0x7BFFu; ++xh) {
-            float xa = ior_f16_to_f32((uint16_t)xh);
-            if (xa > lim) break; /* fp16 bit order is magnitude order */
+            const float xa = ior_f16_to_f32((uint16_t)xh);
+            if (xa > lim) break;
             for (int sg = 0; sg < 2; ++sg) {
-                float x = sg ? -xa : xa;
-                float y = x * r;
-                float e = fmaf(-y, s, x);
-                float y2 = refine ? fmaf(r, e, y) : y;
-                y2 = y2 < -7.0f ? -7.0f : (y2 > 7.0f ? 7.0f : y2);
-                float t = y2 + 12582912.0f;
+                const float x = sg ? -xa : xa;
+                const float t = mode == 2 ? fmaf(x, r, 12582912.0f)
+                                          : fmaf(x, r, 3072.0f) + (12582912.0f - 3072.0f);
                 uint32_t tb;
                 memcpy(&tb, &t, 4);
                 bad += (int)(tb & 0xFu) != (quant_ref(x, s) & 0xF);
             }
+        }
+    }
+    return bad;
+}
+
+/*
+ * Packing: the kernels sum the 8 code bit patterns t_i = 0x4B400000 + k_i
+ * of a group, shifted left by 4i, add 0x11111111 * (8 - 0x4B400000) and
+ * xor 0x88888888 (all mod 2^32).  Count the tuples (k_0..k_7) in [-7, 7]^8
+ * (all 15^8) for which that differs from the nibble packing of
+ * pack_int4 (code i in bits [4i+3:4i], two's complement).  bias_delta is
+ * added to the bias; the tests pass 1 to show that a wrong constant fails.
+ */
+int64_t ior_check_pack_sum(int32_t bias_delta) {
+    const uint32_t bias = 0x11111111u * (8u - 0x4B400000u) + (uint32_t)bias_delta;
+    int64_t bad = 0;
+    int32_t hi;
+#pragma omp parallel for schedule(static) reduction(+ : bad)
+    for (hi = 0; hi < 15 * 15 * 15 * 15; ++hi) {
+        uint32_t acc_hi = 0, want_hi = 0;
+        for (int i = 4, h = hi; i < 8; ++i, h /= 15) {
+            const int k = h % 15 - 7;
+            acc_hi += (0x4B400000u + (uint32_t)k) << (4 * i);
+            want_hi |= ((uint32_t)k & 0xFu) << (4 * i);
+        }
+        for (int lo = 0; lo < 15 * 15 * 15 * 15; ++lo) {
+            uint32_t acc = acc_hi, want = want_hi;
+            for (int i = 0, l = lo; i < 4; ++i, l /= 15) {
+                const int k = l % 15 - 7;
+                acc += (0x4B400000u + (uint32_t)k) << (4 * i);
+                want |= ((uint32_t)k & 0xFu) << (4 * i);
+            }
+            bad += ((acc + bias) ^ 0x88888888u) != want;
         }
     }
     return bad;

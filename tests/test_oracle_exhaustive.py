@@ -41,14 +41,24 @@ def test_scale_multiply_by_one_seventh_is_exact():
     assert c_oracle.check_scale_mul() == 0
 
 
-def test_fast_quantiser_is_exact_for_every_reachable_input():
-    # Every scale the quantiser can emit x every fp16 |x| <= 8 * scale, with
-    # the reciprocal correctly rounded or off by one ulp either way.
-    for rvariant in (0, -1, 1):
-        assert c_oracle.check_quant_fast(rvariant) == 0
+def test_quantiser_is_exact_for_every_reachable_input():
+    # Every scale the quantiser can emit x every fp16 x with |x| up to the
+    # largest group amax giving that scale, with the reciprocal correctly
+    # rounded or off by up to two floats either way.
+    for rvariant in (0, -1, 1, -2, 2):
+        assert c_oracle.check_quant_grid(rvariant) == 0
 
 
-def test_fast_quantiser_check_detects_missing_correction():
-    # Without the fma correction step, exact half-way cases round the wrong
-    # way: the exhaustive check must see them.
-    assert c_oracle.check_quant_fast(0, refine=False) > 0
+def test_quantiser_check_detects_planted_mistakes():
+    # Past the group amax the missing clamp shows; rounding in one step
+    # instead of two gets exact half-way cases wrong.  The exhaustive check
+    # must see both.
+    assert c_oracle.check_quant_grid(0, mode=1) > 0
+    assert c_oracle.check_quant_grid(0, mode=2) > 0
+
+
+def test_shift_and_add_packing_is_exact():
+    # All 15^8 code tuples of a 32-dim group pack to pack_int4's nibbles;
+    # a bias off by one does not.
+    assert c_oracle.check_pack_sum() == 0
+    assert c_oracle.check_pack_sum(1) > 0
