@@ -68,7 +68,7 @@ __device__ __forceinline__ half2_t quad_amax(half2_t m) {
 // block's RPT * kRowsPerBlock.  Loads go out in three waves, each for all RPT
 // rows: the slot and position words, then the K and V chunks, then (once the
 // positions are in) the RoPE table chunks, so the table reads overlap the
-// K/V reads instead of following them.  Large appends use RPT = 2.
+// K/V reads instead of following them.  The launch uses RPT = 1.
 //
 // Row r is (token r / n_heads, head r % n_heads); the quotient is taken as
 // trunc((r + 0.5) * RN64(1 / n_heads)) in fp64, exact for r < 2^31 and
@@ -235,30 +235,29 @@ extern "C" int iris_rope_int4_paged_append(
     int rowlanes = 8;
     while (rowlanes < chunks) rowlanes <<= 1;
     const int64_t rows_per_block = 256 / rowlanes;
-    // Two rows a thread for large appends, one for short appends, which are
-    // latency-bound either way.
-    const int rpt = n_rows >= 65536 ? 2 : 1;
-    const int64_t blocks = (n_rows + rows_per_block * rpt - 1) / (rows_per_block * rpt);
+    // One row a thread: the config-5 bulk append (4 x 8192 tokens, Hkv=8,
+    // D=128) takes 32.0 us on MI355X against 33.6 with two rows a thread and
+    // 34.7 with four, and 32.9 / 32.5 / 35.3 us with 128 / 512 / 1024-thread
+    // blocks.
+    const int64_t blocks = (n_rows + rows_per_block - 1) / rows_per_block;
     hipStream_t s = (hipStream_t)stream;
     const bool per_elem = rotary_dim % 16 != 0;
     const bool ror8 = rowlanes == 16 && rotary_dim == 128;
     const double inv_heads = 1.0 / (double)num_kv_heads;
     if (rotary_dim == 0) cos_cache = sin_cache = key;  // a readable 16 bytes; the values are not used
-#define IRIS_LAUNCH_APPEND(RL, RPT, PE, ROR)                                                                   \
-    hipLaunchKernelGGL((rope_int4_paged_append_kernel<RL, RPT, PE, ROR>), dim3((unsigned)blocks), dim3(256), 0, s, \
+#define IRIS_LAUNCH_APPEND(RL, PE, ROR)                                                                      \
+    hipLaunchKernelGGL((rope_int4_paged_append_kernel<RL, 1, PE, ROR>), dim3((unsigned)blocks), dim3(256), 0, s, \
                        (const u32x4_t*)key, (const u32x4_t*)value, positions, slot_mapping,                     \
                        (const half_t*)cos_cache, (const half_t*)sin_cache, (u32x4_t*)k_data,                    \
                        (u32x4_t*)v_data, (uint32_t*)k_scale, (uint32_t*)v_scale, (int)n_rows,                   \
                        (int)num_kv_heads, inv_heads, (int)head_dim, (int)rotary_dim)
-#define IRIS_LAUNCH_APPEND_RPT(RL)                          \
-    if (per_elem) IRIS_LAUNCH_APPEND(RL, 1, true, false);   \
-    else if (rpt == 2) IRIS_LAUNCH_APPEND(RL, 2, false, false); \
-    else IRIS_LAUNCH_APPEND(RL, 1, false, false)
+#define IRIS_LAUNCH_APPEND_RPT(RL)                 \
+    if (per_elem) IRIS_LAUNCH_APPEND(RL, true, false); \
+    else IRIS_LAUNCH_APPEND(RL, false, false)
     switch (rowlanes) {
         case 8: IRIS_LAUNCH_APPEND_RPT(8); break;
         case 16:
-            if (ror8 && rpt == 2) IRIS_LAUNCH_APPEND(16, 2, false, true);
-            else if (ror8) IRIS_LAUNCH_APPEND(16, 1, false, true);
+            if (ror8) IRIS_LAUNCH_APPEND(16, false, true);
             else IRIS_LAUNCH_APPEND_RPT(16);
             break;
         case 32: IRIS_LAUNCH_APPEND_RPT(32); break;
