@@ -17,8 +17,8 @@
 // (D=128: 4 rows of 16 lanes).  With 8 dims per lane, the 4 lanes of a quad
 // are exactly one 32-dim scale group, so the group amax is two quad
 // shuffles.  Consecutive rows are consecutive heads of one token, whose
-// cache rows are adjacent in the NHD page layout, so the 32-bit code stores
-// of a wave cover whole cache lines.
+// cache rows are adjacent in the NHD page layout, so the code stores of a
+// wave cover whole cache rows.
 //
 // RoPE (rotate-half, as torch_eager_kv.py:38-47) on the first R = rotary_dim
 // dims: dim i < R/2 pairs with i + R/2.  When R is a multiple of 16 every
