@@ -79,7 +79,8 @@ def decode_kernel_name(plan, group: int, n_kv: int, d: int, batch: int, max_page
     IRIS_DECODE_KERNEL=valu)."""
     if (plan[2] == 16 and plan[0] > 0 and plan[1] <= 64 and d == 128 and n_kv == 8 and group == 4
             and os.environ.get("IRIS_DECODE_KERNEL") != "pages"):
-        return "void iris::st::int4_decode_stream_kernel<8>(iris::st::Args)"
+        # (rocprofv3 prints this kernel mangled: _Float16 in its signature)
+        return "_ZN4iris2st25int4_decode_stream_kernelILi8EEEvPKiS3_PKDF16_iiiiiiiNS0_4ArgsE"
     if plan[2] == 16:
         gs = 4
         while gs > 1 and gs * group > 16:

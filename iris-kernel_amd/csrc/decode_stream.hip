@@ -17,7 +17,7 @@
 // * a workgroup of 16 waves owns (sequence, chunk of 32-token tiles) and
 //   reads every kv head of each page;
 // * every load moves 1 KiB straight into LDS (buffer_load ... lds);
-// * a ring of four slots, three in flight.  Slot s holds the K pages and K
+// * a ring of four slots, two in flight.  Slot s holds the K pages and K
 //   scales of tile s and the V pages and V scales of tile s - 1 (36 loads:
 //   each wave one K and one V load, waves 0-3 one scale load each).
 //
@@ -65,7 +65,7 @@ constexpr int kTile = 32;
 constexpr int kPage = 16;
 constexpr int kWaves = 16;
 constexpr int kSlots = 4;           // ring slots
-constexpr int kAhead = kSlots - 1;  // slots in flight
+constexpr int kAhead = 2;           // slots in flight (three measured 0.4 us slower at cfg2)
 constexpr int kJobs = 3;            // loads per wave per slot
 constexpr int kMaxChunkTiles = 64;  // a chunk's 128 page ids fill two VGPRs
 constexpr int kMaxChunks = 64;      // partials the merge reads
@@ -259,7 +259,13 @@ __device__ __forceinline__ void store2_sc1(float2v_t v, const __amdgpu_buffer_rs
 }
 
 template <int HKV>
-__global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(Args a) {
+// The scalars the prologue needs come first, as separate arguments: built
+// with -mllvm -amdgpu-kernarg-preload-count=10 they arrive in SGPRs with the
+// wave, so the sequence-length and block-table loads do not wait for a
+// kernel-argument load first (the Args copies are the same values).
+__global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
+    const int32_t* p_seq_lens, const int32_t* p_block_table, const half_t* p_q, int p_max_chunks, int p_chunk_tiles,
+    int p_bt_cols, int p_max_pages, int p_page_shift, int p_n_q_heads, int p_nblocks, Args a) {
     using L = Geo<HKV>;
     constexpr int D = L::D, GQ = L::GQ, G = L::G, CK = L::CK, SLOT = L::SLOT;
     constexpr uint32_t KPAGE = L::KPAGE, SPAGE = L::SPAGE;
@@ -276,23 +282,23 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(Args a)
     const int jq = lane >> 4;  // MFMA k-chunk (A, B) or row quad (C)
     const int kvh = wave % HKV, par = wave / HKV;  // kv head; tiles of this parity
 
-    const int wg = xcd_remap(blockIdx.x, gridDim.x);
-    const int b = wg / a.max_chunks, chunk = wg % a.max_chunks;
-    const int t_begin = chunk * a.chunk_tiles;
+    const int wg = xcd_remap(blockIdx.x, p_nblocks);
+    const int b = wg / p_max_chunks, chunk = wg % p_max_chunks;
+    const int t_begin = chunk * p_chunk_tiles;
     const int p0 = 2 * t_begin;
-    const int seq_len = a.seq_lens[b];
+    const int seq_len = p_seq_lens[b];
 
     // ---- page ids of the chunk (logical page p0 + i in lane i of pid0 /
     // pid1) and the raw query rows: neither depends on the sequence length,
     // so they are in flight together with its load.
-    const int32_t* bt = a.block_table + (int64_t)b * a.bt_cols;
+    const int32_t* bt = p_block_table + (int64_t)b * p_bt_cols;
     // (every lane loads, clamped into the table; no divergent branches
     // around the loads, so none waits for another)
-    int pid0 = virtual_page(bt, min(p0 + lane, a.max_pages - 1), a.page_shift);
-    int pid1 = virtual_page(bt, min(p0 + 64 + lane, a.max_pages - 1), a.page_shift);
+    int pid0 = virtual_page(bt, min(p0 + lane, p_max_pages - 1), p_page_shift);
+    int pid1 = virtual_page(bt, min(p0 + 64 + lane, p_max_pages - 1), p_page_shift);
     // Query A operand: row n = (h, g) = (n >> 2, n & 3), nonzero only where
     // g == jq: 32 dims of group jq of head h.
-    const half_t* qh = a.q + ((int64_t)b * a.n_q_heads + kvh * GQ) * D;
+    const half_t* qh = p_q + ((int64_t)b * p_n_q_heads + kvh * GQ) * D;
     u32x4_t qraw[4];
     {
         const half_t* qrow = qh + (n >> 2) * D + 32 * jq;
@@ -303,9 +309,9 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(Args a)
 
     const int n_tiles = (seq_len + kTile - 1) / kTile;
     if (t_begin >= n_tiles) return;  // uniform over the workgroup
-    const int t_end = min(t_begin + a.chunk_tiles, n_tiles);
+    const int t_end = min(t_begin + p_chunk_tiles, n_tiles);
     const int n_stages = t_end - t_begin;
-    const int n_chunks = (n_tiles + a.chunk_tiles - 1) / a.chunk_tiles;
+    const int n_chunks = (n_tiles + p_chunk_tiles - 1) / p_chunk_tiles;
     const int last_lp = (seq_len + kPage - 1) / kPage - 1;
 
     // ---- this wave's three loads of a slot (the same every step); each
@@ -590,7 +596,7 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(Args a)
     // ---- the chunk's result for element idx = (kv head, query head, dim),
     // 4 dims at a time: the two sets' states combined.  A set without tiles
     // (a one-tile chunk) has m = -inf, l = 0, o = 0 and weight 0.
-    const int hq = a.n_q_heads;
+    const int hq = p_n_q_heads;
     const int total = hq * D, n4 = total / 4;
     auto chunk4 = [&](int e4, float& m, float& l) -> float4_t {
         const int idx = 4 * e4;
@@ -625,7 +631,7 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(Args a)
     // ---- split-KV: publish (o / l, m, l) with device-coherent stores; the
     // last chunk to arrive merges every chunk of the sequence.
     const uint32_t part_o = (uint32_t)total * 4, part_ml = (uint32_t)hq * 8;  // bytes per partial
-    const int64_t row0 = (int64_t)b * a.max_chunks;
+    const int64_t row0 = (int64_t)b * p_max_chunks;
     {
         const auto ro = buf_rsrc(a.part_o + (row0 + chunk) * total, part_o);
         const auto rm = buf_rsrc(a.part_ml + (row0 + chunk) * hq * 2, part_ml);
@@ -710,7 +716,8 @@ int launch_stream(dim3 grid, hipStream_t s, const st::Args& a) {
     static std::atomic<uint64_t> lds_raised{0};
     if (allow_full_lds(reinterpret_cast<const void*>(&st::int4_decode_stream_kernel<HKV>), lds_raised) != kOk)
         return kLaunchError;
-    hipLaunchKernelGGL((st::int4_decode_stream_kernel<HKV>), grid, dim3(64 * st::kWaves), lds, s, a);
+    hipLaunchKernelGGL((st::int4_decode_stream_kernel<HKV>), grid, dim3(64 * st::kWaves), lds, s, a.seq_lens, a.block_table, a.q,
+                       a.max_chunks, a.chunk_tiles, a.bt_cols, a.max_pages, a.page_shift, a.n_q_heads, (int)grid.x, a);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchError;
 }
 

@@ -28,7 +28,8 @@ SOURCES = {
     "append.hip": ["-ffp-contract=off"],
     "decode.hip": [],
     "decode_pages.hip": [],
-    "decode_stream.hip": [],
+    # the streaming kernel takes its prologue scalars in preloaded SGPRs
+    "decode_stream.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=10"],
     "decode_fp16.hip": [],
     "kv_fp16.hip": ["-ffp-contract=off"],
     "check.hip": [],
