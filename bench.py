@@ -74,13 +74,15 @@ def append_bytes(n_tok, n_kv, d, n_pos) -> int:
 def decode_kernel_name(plan, group: int, n_kv: int, d: int, batch: int, max_pages: int) -> str:
     """Name of the decode kernel a plan runs, as rocprofv3 reports it.  16-wave
     plans: the streaming kernel for its shape (D=128, Hkv=8, 4 query heads per
-    kv head) in chunk mode with at most 64 chunks, else the page-streaming
-    kernel; other plans: the general kernel (its VALU-tile variant with
+    kv head) in chunk mode with at most 64 chunks, the MQA streaming kernel for
+    one kv head at D=64, else the page-streaming kernel; other plans: the general kernel (its VALU-tile variant with
     IRIS_DECODE_KERNEL=valu)."""
     if (plan[2] == 16 and plan[0] > 0 and plan[1] <= 64 and d == 128 and n_kv == 8 and group == 4
             and os.environ.get("IRIS_DECODE_KERNEL") != "pages"):
         # (rocprofv3 prints this kernel mangled: _Float16 in its signature)
         return "_ZN4iris2st25int4_decode_stream_kernelILi8EEEvPKiS3_PKDF16_iiiiiiiNS0_4ArgsE"
+    if plan[2] == 16 and n_kv == 1 and d == 64 and group <= 16 and os.environ.get("IRIS_DECODE_KERNEL") != "pages":
+        return "iris::mq::int4_decode_mqa_kernel(iris::mq::Args)"
     if plan[2] == 16:
         gs = 4
         while gs > 1 and gs * group > 16:

@@ -64,6 +64,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "decode_mqa.h"
 #include "decode_pages.h"
 #include "iris_hip.h"
 
@@ -1369,6 +1370,24 @@ static bool pages_preferred(int64_t batch, int64_t num_q_heads, int64_t num_kv_h
     return lengths_known || 4 * total_tokens >= 3 * batch * max_tokens;
 }
 
+// The MQA streaming kernel (decode_mqa.hip: one kv head, head_dim 64, at
+// most 16 query heads) takes 16-wave plans of its shape.  Left to choose, the
+// plan takes it for batches of similar lengths with at least kMqaMinBytes of
+// K/V to read (configuration 4: B=128, L=8192, 76 MB); smaller or ragged
+// batches go to the general kernel's many small chunks.
+// IRIS_DECODE_KERNEL=pages forces the page kernel for A/B runs.
+constexpr int64_t kMqaMinBytes = 16000000;
+static bool mqa_allowed(int32_t waves_per_block) {
+    const char* sel = getenv("IRIS_DECODE_KERNEL");
+    if (sel != nullptr && (strcmp(sel, "general") == 0 || strcmp(sel, "valu") == 0 || strcmp(sel, "pages") == 0))
+        return false;
+    return waves_per_block <= 0 || waves_per_block == mqa_waves();
+}
+static bool mqa_preferred(int64_t batch, int64_t total_tokens, int64_t max_tokens) {
+    if (total_tokens * (64 + 8) < kMqaMinBytes) return false;
+    return 4 * total_tokens >= 3 * batch * max_tokens;
+}
+
 // Split plan for one decode call.  total_tokens / max_tokens may be -1 when
 // the caller does not know the sequence lengths; max_pages bounds them.
 extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
@@ -1384,6 +1403,11 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
     // block_table admits stands in for them.
     const int64_t est_max = max_tokens < 0 ? max_pages * kPageSize : max_tokens;
     const int64_t est_total = total_tokens < 0 ? batch * est_max : total_tokens;
+    if (mqa_allowed(waves_per_block) && mqa_supported(num_q_heads, num_kv_heads, head_dim) &&
+        (waves_per_block == mqa_waves() || mqa_preferred(batch, est_total, est_max)) &&
+        mqa_plan(batch, num_q_heads, head_dim, max_pages, max_tokens, tokens_per_split, out_chunk_tiles,
+                 out_max_chunks, out_waves, out_workspace_bytes) == kOk)
+        return kOk;
     if (pages_allowed(waves_per_block) && pages_supported(num_q_heads, num_kv_heads, head_dim, max_pages) &&
         (waves_per_block == pages_waves() ||
          pages_preferred(batch, num_q_heads, num_kv_heads, head_dim, est_total, est_max,
@@ -1463,6 +1487,11 @@ extern "C" int iris_int4_paged_decode_attention(
         return kInvalidArgument;
     const int64_t bt_cols = max_pages;
     max_pages <<= shift;
+    if (waves_per_block == mqa_waves() && mqa_allowed(waves_per_block) &&
+        mqa_supported(num_q_heads, num_kv_heads, head_dim) && chunk_tiles > 0)
+        return mqa_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
+                          workspace, workspace_bytes_avail, batch, num_q_heads, max_pages, bt_cols, shift,
+                          softmax_scale, chunk_tiles, max_chunks, stream);
     if (waves_per_block == pages_waves() && pages_allowed(waves_per_block) &&
         pages_supported(num_q_heads, num_kv_heads, head_dim, max_pages))
         return pages_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,

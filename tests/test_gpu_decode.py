@@ -451,6 +451,88 @@ def test_wider_scope_matches_eager(device, kernel, hq, hkv, d, page, lens, tps):
     assert_attention_close(out, want, f"Hq={hq} Hkv={hkv} D={d} P={page}")
 
 
+# ------------------------------------------------------------------ MQA streaming kernel
+# One kv head, head_dim 64, at most 16 query heads: 16-wave plans run the MQA
+# streaming kernel (decode_mqa.hip).  Ragged lengths (partial tiles and
+# pages, a one-token sequence, steps with fewer tiles than waves), splits of
+# 1 to many chunks, fewer query heads than MFMA columns, pages of 16 << k
+# tokens, fp32 and fp16 outputs.
+@pytest.mark.parametrize("hq,page,lens,tps", [
+    (16, 16, [8192, 8192, 8192], 0),          # configuration 4's shape, plan's split
+    (16, 16, [1, 17, 33, 511, 4097], 0),
+    (16, 16, [1, 17, 33, 511, 4097], 512),    # 16-tile chunks: many per sequence
+    (16, 16, [3000, 70, 9000], 1536),         # chunks of 48 tiles (three steps)
+    (8, 16, [600, 2500], 0),                  # half the columns
+    (3, 16, [129, 1000, 31], 512),
+    (1, 16, [2000], 0),
+    (16, 32, [40, 1000, 3000], 0),            # 32-token pages
+    (12, 128, [130, 5000], 1024),             # 128-token pages
+])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+def test_mqa_kernel_matches_eager(device, hq, page, lens, tps, out_dtype):
+    log(f"decode mqa: Hq={hq} P={page} lens={lens} split={tps} out={out_dtype}")
+    g = torch.Generator().manual_seed(hq * 11 + page + len(lens) + tps)
+    B = len(lens)
+    max_pages = max(-(-n // page) for n in lens) + 1
+    num_pages = B * max_pages + 2
+    kd, vd, ks, vs = _quantized_pool(num_pages, page, 1, 64, g)
+    bt = torch.randperm(num_pages, generator=g)[: B * max_pages].view(B, max_pages).to(torch.int32)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    q = torch.randn(B, hq, 64, generator=g).to(torch.float16)
+    want = torch_eager_int4_paged_decode_attention(q, kd, vd, ks, vs, bt, sl, page_size=page,
+                                                   out_dtype=torch.float32)
+    plan = decode_plan(B, hq, 1, 64, max_pages * (page // 16), sum(lens), max(lens), tps, 16)
+    assert plan[2] == 16 and plan[0] % 16 == 0, plan  # the MQA kernel's plan: whole steps of 16 tiles
+    qg, btg, slg = to(device, q, bt, sl)
+    cache = to(device, kd, vd, ks, vs)
+    out = torch.empty(q.shape, dtype=out_dtype, device=device)
+    fused_int4_paged_decode_attention(qg, *cache, btg, slg, out, page_size=page, tokens_per_split=tps,
+                                      waves_per_block=16)
+    torch.cuda.synchronize(device)
+    assert_attention_close(out.cpu(), want if out_dtype == torch.float32 else want.to(torch.float16),
+                           f"mqa Hq={hq} P={page} lens={lens}")
+
+
+def test_mqa_kernel_nan_tail_and_repeat(device):
+    # Slots past each sequence's length hold NaN scales and random codes: the
+    # output must not change; a second launch on the same workspace (the
+    # arrival counters back at zero) gives the identical result.
+    g = torch.Generator().manual_seed(4242)
+    lens = [4100, 30, 777]
+    B, hq, page = len(lens), 16, 16
+    max_pages = max(-(-n // page) for n in lens) + 1
+    num_pages = B * max_pages + 2
+    kd, vd, ks, vs = _quantized_pool(num_pages, page, 1, 64, g)
+    bt = torch.randperm(num_pages, generator=g)[: B * max_pages].view(B, max_pages).to(torch.int32)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    q = torch.randn(B, hq, 64, generator=g).to(torch.float16)
+    want = torch_eager_int4_paged_decode_attention(q, kd, vd, ks, vs, bt, sl, page_size=page,
+                                                   out_dtype=torch.float32)
+    qg, btg, slg = to(device, q, bt, sl)
+
+    def launch(cache):
+        out = torch.empty(q.shape, dtype=torch.float32, device=device)
+        fused_int4_paged_decode_attention(qg, *to(device, *cache), btg, slg, out, tokens_per_split=512,
+                                          waves_per_block=16)
+        torch.cuda.synchronize(device)
+        return out.cpu()
+
+    clean = launch((kd, vd, ks, vs))
+    assert_attention_close(clean, want, "mqa clean")
+    assert torch.equal(launch((kd, vd, ks, vs)), clean)
+    kd, vd, ks, vs = (t.clone() for t in (kd, vd, ks, vs))
+    for b, n in enumerate(lens):
+        last = int(bt[b, (n - 1) // page])
+        tail = slice(n % page if n % page else page, page)
+        ks[last, tail] = float("nan")
+        vs[last, tail] = float("nan")
+        kd[last, tail] = torch.randint(0, 256, kd[last, tail].shape, dtype=torch.uint8, generator=g)
+        vd[last, tail] = torch.randint(0, 256, vd[last, tail].shape, dtype=torch.uint8, generator=g)
+    poisoned = launch((kd, vd, ks, vs))
+    assert torch.isfinite(poisoned).all()
+    assert torch.equal(poisoned, clean)
+
+
 # ------------------------------------------------------------------ VALU tile
 # IRIS_DECODE_KERNEL=valu: the general kernel with v_dot2c chains (DPP row
 # broadcasts) in place of its MFMAs -- the alternative the MFMA tile is
