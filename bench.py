@@ -82,7 +82,7 @@ def decode_kernel_name(plan, group: int, n_kv: int, d: int, batch: int, max_page
         # (rocprofv3 prints this kernel mangled: _Float16 in its signature)
         return "_ZN4iris2st25int4_decode_stream_kernelILi8EEEvPKiS3_PKDF16_iiiiiiiNS0_4ArgsE"
     if plan[2] == 16 and n_kv == 1 and d == 64 and group <= 16 and os.environ.get("IRIS_DECODE_KERNEL") != "pages":
-        return "iris::mq::int4_decode_mqa_kernel(iris::mq::Args)"
+        return "_ZN4iris2mq22int4_decode_mqa_kernelEPKiS2_PKDF16_iiiiiiNS0_4ArgsE"  # (printed mangled)
     if plan[2] == 16:
         gs = 4
         while gs > 1 and gs * group > 16:

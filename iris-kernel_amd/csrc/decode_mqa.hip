@@ -34,7 +34,9 @@
 //   sit in the four 16-lane rows of its column;
 // * PV: O^T[d][h] += V codes transposed (A, ds_read_b64_tr_b8) x (p *
 //   v_scale rounded once to fp16, B).  The C layout of S^T is the B layout
-//   of PV, so p never moves between lanes.
+//   of PV, so p never moves between lanes.  The V codes' +8 offset is a
+//   fifth MFMA per group (a constant A operand times the same B), so the
+//   weights are never summed on the VALU.
 // The 16 waves' softmax states are combined through LDS at the end.
 //
 // Split-KV: sequences longer than one chunk publish (m, l, o / l) per query
@@ -171,32 +173,27 @@ __device__ __forceinline__ int lds_i32(uint32_t addr) {
     asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
     return v;
 }
-// K of a tile (four dwords, (half e, group g) 256 bytes apart) and its K
-// scales (two 16-byte reads, page e 64 bytes apart).
-__device__ __forceinline__ void lds_k_reads(uint32_t k, uint32_t ks, uint32_t (&kw)[4], u32x4_t (&ksc)[2]) {
+// All of a tile's reads at once: K (four dwords, (half e, group g) 256
+// bytes apart), K and V scales (16 bytes of page e, 64 bytes apart) and the
+// transposed V reads of both groups.
+__device__ __forceinline__ void lds_tile_reads(uint32_t k, uint32_t ks, uint32_t vs, uint32_t v0, uint32_t v1,
+                                               uint32_t (&kw)[4], u32x4_t (&ksc)[2], u32x4_t (&vsc)[2],
+                                               int2v_t (&w)[2]) {
     asm volatile(
-        "ds_read_b32 %0, %6\n\t"
-        "ds_read_b32 %1, %6 offset:256\n\t"
-        "ds_read_b32 %2, %6 offset:512\n\t"
-        "ds_read_b32 %3, %6 offset:768\n\t"
-        "ds_read_b128 %4, %7\n\t"
-        "ds_read_b128 %5, %7 offset:64\n\t"
+        "ds_read_b32 %0, %10\n\t"
+        "ds_read_b32 %1, %10 offset:256\n\t"
+        "ds_read_b32 %2, %10 offset:512\n\t"
+        "ds_read_b32 %3, %10 offset:768\n\t"
+        "ds_read_b128 %4, %11\n\t"
+        "ds_read_b128 %5, %11 offset:64\n\t"
+        "ds_read_b128 %6, %12\n\t"
+        "ds_read_b128 %7, %12 offset:64\n\t"
+        "ds_read_b64_tr_b8 %8, %13\n\t"
+        "ds_read_b64_tr_b8 %9, %14\n\t"
         "s_waitcnt lgkmcnt(0)"
-        : "=&v"(kw[0]), "=&v"(kw[1]), "=&v"(kw[2]), "=&v"(kw[3]), "=&v"(ksc[0]), "=&v"(ksc[1])
-        : "v"(k), "v"(ks)
-        : "memory");
-}
-// V scales of a tile and the transposed V reads of both groups.
-__device__ __forceinline__ void lds_v_reads(uint32_t vs, uint32_t v0, uint32_t v1, u32x4_t (&vsc)[2],
-                                            int2v_t (&w)[2]) {
-    asm volatile(
-        "ds_read_b128 %0, %4\n\t"
-        "ds_read_b128 %1, %4 offset:64\n\t"
-        "ds_read_b64_tr_b8 %2, %5\n\t"
-        "ds_read_b64_tr_b8 %3, %6\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(vsc[0]), "=&v"(vsc[1]), "=&v"(w[0]), "=&v"(w[1])
-        : "v"(vs), "v"(v0), "v"(v1)
+        : "=&v"(kw[0]), "=&v"(kw[1]), "=&v"(kw[2]), "=&v"(kw[3]), "=&v"(ksc[0]), "=&v"(ksc[1]), "=&v"(vsc[0]),
+          "=&v"(vsc[1]), "=&v"(w[0]), "=&v"(w[1])
+        : "v"(k), "v"(ks), "v"(vs), "v"(v0), "v"(v1)
         : "memory");
 }
 
@@ -210,42 +207,48 @@ __device__ __forceinline__ float load_sc1(const float* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(Args a) {
+// The scalars the prologue needs come first, as separate arguments: built
+// with -mllvm -amdgpu-kernarg-preload-count=9 they arrive in SGPRs with the
+// wave, so the page-id and sequence-length loads do not wait for a
+// kernel-argument load first (the Args copies are the same values).
+__global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
+    const int32_t* p_seq_lens, const int32_t* p_block_table, const half_t* p_q, int p_max_chunks, int p_chunk_tiles,
+    int p_bt_cols, int p_max_pages, int p_page_shift, int p_n_q_heads, Args a) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 15;   // MFMA row (A) or column (B, C): token or query head
     const int jq = lane >> 4;  // MFMA k-chunk (A, B) or row quad (C)
 
-    const int b = blockIdx.x / a.max_chunks, chunk = blockIdx.x % a.max_chunks;
-    const int t_begin = chunk * a.chunk_tiles;
+    const int b = blockIdx.x / p_max_chunks, chunk = blockIdx.x % p_max_chunks;
+    const int t_begin = chunk * p_chunk_tiles;
     const int p0 = 2 * t_begin;  // first 16-token page of the chunk
-    const int32_t* bt = a.block_table + (int64_t)b * a.bt_cols;
+    const int32_t* bt = p_block_table + (int64_t)b * p_bt_cols;
 
     // ---- the chunk's page ids (thread j: page p0 + j, clamped into the
     // table row) and q are in flight together with the sequence length.
-    const int n_pid = 2 * a.chunk_tiles;
+    const int n_pid = 2 * p_chunk_tiles;
     int raw_pid = 0;
-    if ((int)threadIdx.x < n_pid) raw_pid = virtual_page(bt, min(p0 + (int)threadIdx.x, a.max_pages - 1), a.page_shift);
+    if ((int)threadIdx.x < n_pid) raw_pid = virtual_page(bt, min(p0 + (int)threadIdx.x, p_max_pages - 1), p_page_shift);
     // q as the QK B operand: lane (head n, k-chunk jq) holds dims
     // 32 g + 8 jq .. + 7 of head n (zero for n >= the query heads).
-    const bool col_valid = n < a.n_q_heads;
+    const bool col_valid = n < p_n_q_heads;
     u32x4_t qraw[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         qraw[g] = u32x4_t{0, 0, 0, 0};
         if (col_valid)
-            qraw[g] = *reinterpret_cast<const u32x4_t*>(a.q + ((int64_t)b * a.n_q_heads + n) * D + 32 * g + 8 * jq);
+            qraw[g] = *reinterpret_cast<const u32x4_t*>(p_q + ((int64_t)b * p_n_q_heads + n) * D + 32 * g + 8 * jq);
     }
-    const int seq_len = a.seq_lens[b];
+    const int seq_len = p_seq_lens[b];
     asm volatile("" ::: "memory");  // keeps the loads above issued before the early return below
 
     const int n_tiles = (seq_len + kTile - 1) / kTile;
     if (t_begin >= n_tiles) return;  // uniform over the workgroup
-    const int t_end = min(t_begin + a.chunk_tiles, n_tiles);
+    const int t_end = min(t_begin + p_chunk_tiles, n_tiles);
     const int n_ct = t_end - t_begin;
     const int n_steps = (n_ct + kWaves - 1) / kWaves;
-    const int n_chunks = (n_tiles + a.chunk_tiles - 1) / a.chunk_tiles;
+    const int n_chunks = (n_tiles + p_chunk_tiles - 1) / p_chunk_tiles;
     const int last_lp = (seq_len + 15) / 16 - 1;
     // Table entries past jlim (pages past the sequence or the chunk) are
     // never read: a lookup is clamped to the last page that holds tokens.
@@ -334,13 +337,17 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(Args a) {
     const float lazy = 2.0f / c24;                 // rescale when a maximum grows by more (base 2)
     float m_run = -INFINITY;                       // MFMA units
     float l_part = 0.0f;
-    float ps[G];  // sums of the PV weights per group (V code offset)
+    // oc8[g]: 8 * 2^-24 * (sum of the PV weights of group g) in every row,
+    // the V code offset, accumulated by an MFMA with a constant A operand.
+    float4_t oc8[G];
     float4_t o[G][2];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        ps[g] = 0.0f;
+        oc8[g] = float4_t{0, 0, 0, 0};
         o[g][0] = o[g][1] = float4_t{0, 0, 0, 0};
     }
+    const _Float16 c8 = __builtin_bit_cast(_Float16, (uint16_t)8);  // 8 * 2^-24, an exact subnormal
+    const half8_t a8 = {c8, c8, c8, c8, c8, c8, c8, c8};
 
     // One tile whose slot has landed: s[e][i] is token 16 e + 4 jq + i,
     // query head n.
@@ -348,8 +355,9 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(Args a) {
         const int tok0 = tile * kTile;
         const bool full = tok0 + kTile <= seq_len;
         uint32_t kw[4];
-        u32x4_t ksc[2];
-        lds_k_reads(base + k_rd, base + ks_rd, kw, ksc);
+        u32x4_t ksc[2], vsc[2];
+        int2v_t vw[2];
+        lds_tile_reads(base + k_rd, base + ks_rd, base + vs_rd, base + tr0, base + tr1, kw, ksc, vsc, vw);
         float s[2][4];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
@@ -382,7 +390,7 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(Args a) {
             l_part *= alpha;
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                ps[g] *= alpha;
+                oc8[g] *= alpha;
                 o[g][0] *= alpha;
                 o[g][1] *= alpha;
             }
@@ -396,9 +404,6 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(Args a) {
                 p[e][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e][i], c24, moff));
                 l_part += p[e][i];
             }
-        u32x4_t vsc[2];
-        int2v_t vw[2];
-        lds_v_reads(base + vs_rd, base + tr0, base + tr1, vsc, vw);
         uint32_t vsd[2][4];
 #pragma unroll
         for (int e = 0; e < 2; ++e)
@@ -414,7 +419,6 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(Args a) {
                 for (int i = 0; i < 4; ++i)
                     if (16 * e + i >= nval) vsd[e][i] = 0u;
         }
-        const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             half8_t bp;
@@ -423,9 +427,7 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(Args a) {
                 const int e = kVSlotByte[sl] >> 2, i = kVSlotByte[sl] & 3;
                 bp[sl] = (half_t)__builtin_fmaf(p[e][i], (float)as_half2(vsd[e][i])[g], 0.0f);
             }
-#pragma unroll
-            for (int qq = 0; qq < 4; ++qq)
-                ps[g] = __builtin_amdgcn_fdot2(half2_t{bp[2 * qq], bp[2 * qq + 1]}, one2, ps[g], false);
+            oc8[g] = mfma16x16x32(a8, bp, oc8[g]);
             half8_t lo, hi;
             v_operands(vw[g], lo, hi);
             o[g][0] = mfma16x16x32(lo, bp, o[g][0]);
@@ -453,7 +455,7 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(Args a) {
         l_part = row_sum4(l_part);
         float psr[G];
 #pragma unroll
-        for (int g = 0; g < G; ++g) psr[g] = 8.0f * row_sum4(ps[g]);
+        for (int g = 0; g < G; ++g) psr[g] = oc8[g][0] * 16777216.0f;
         float* const ep = reinterpret_cast<float*>(smem) + wave * EPI_FLOATS;
         if (jq == 0) {
             ep[n] = m_run * c24;
@@ -488,7 +490,7 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(Args a) {
     }
     oc *= 1.0f / lc;
 
-    const int hq = a.n_q_heads;
+    const int hq = p_n_q_heads;
     auto store_out = [&](float v) {
         if (h >= hq) return;
         const int64_t idx = ((int64_t)b * hq + h) * D + d;
@@ -503,7 +505,7 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(Args a) {
     // ---- split-KV: publish (o / l, m, l) with device-coherent stores; the
     // last chunk to arrive (the protocol of arrive_last) merges every chunk
     // of the sequence.
-    const int64_t row0 = (int64_t)b * a.max_chunks;
+    const int64_t row0 = (int64_t)b * p_max_chunks;
     store_sc1(oc, a.part_o + (row0 + chunk) * (16 * D) + threadIdx.x);
     if (d == 0) {
         store_sc1(mc, a.part_ml + ((row0 + chunk) * 16 + h) * 2);
@@ -649,7 +651,8 @@ int mqa_launch(const void* query, const void* k_data, const void* v_data, const 
     if (allow_full_lds(reinterpret_cast<const void*>(&mq::int4_decode_mqa_kernel), lds_raised) != kOk)
         return kLaunchError;
     hipLaunchKernelGGL(mq::int4_decode_mqa_kernel, dim3((unsigned)nblocks), dim3(64 * mq::kWaves), mq::LDS_BYTES,
-                       (hipStream_t)stream, a);
+                       (hipStream_t)stream, a.seq_lens, a.block_table, a.q, a.max_chunks, a.chunk_tiles, a.bt_cols,
+                       a.max_pages, a.page_shift, a.n_q_heads, a);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchError;
 }
 

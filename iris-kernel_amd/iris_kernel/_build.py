@@ -30,7 +30,7 @@ SOURCES = {
     "decode_pages.hip": [],
     # the streaming kernel takes its prologue scalars in preloaded SGPRs
     "decode_stream.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=10"],
-    "decode_mqa.hip": [],
+    "decode_mqa.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
     "decode_fp16.hip": [],
     "kv_fp16.hip": ["-ffp-contract=off"],
     "check.hip": [],
