@@ -160,7 +160,7 @@ def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path shards "
-              "by kv head or by page range with no exchange; see DESIGN.md)", file=sys.stderr)
+              "by kv head, or by page range with one all-gather of the fp32 partials per layer)", file=sys.stderr)
         return 2
     import torch
 
