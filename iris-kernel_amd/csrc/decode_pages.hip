@@ -1172,11 +1172,11 @@ int pages_launch(const void* query, const void* k_data, const void* v_data, cons
     const bool balanced = chunk_tiles < 0;
     const int64_t share = balanced ? -(int64_t)chunk_tiles : chunk_tiles;
     if (share <= 0 || share > pg::kMaxChunkTiles || max_chunks <= 0) return kInvalidArgument;
-    // Chunk mode of the shapes the streaming kernel has (decode_stream.hip):
-    // it runs them instead (IRIS_DECODE_KERNEL=pages keeps this kernel, for
-    // A/B measurements).  Its workspace is no larger than this kernel's.
-    if (!balanced && stream_supported(num_q_heads, num_kv_heads, head_dim) && max_chunks <= stream_max_chunks() &&
-        stream_allowed())
+    // The shapes the streaming kernel has (decode_stream.hip), in either
+    // mode: it runs them instead (IRIS_DECODE_KERNEL=pages keeps this kernel,
+    // for A/B measurements).  Its workspace layout is this kernel's.
+    if (stream_supported(num_q_heads, num_kv_heads, head_dim) &&
+        (balanced ? max_chunks <= 8 * pg::kMaxGroups : max_chunks <= stream_max_chunks()) && stream_allowed())
         return stream_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
                              workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, max_pages,
                              bt_cols, page_shift, softmax_scale, chunk_tiles, max_chunks, stream);

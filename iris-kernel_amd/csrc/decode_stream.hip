@@ -70,6 +70,10 @@ constexpr int kJobs = 3;            // loads per wave per slot
 constexpr int kMaxChunkTiles = 64;  // a chunk's 128 page ids fill two VGPRs
 constexpr int kMaxChunks = 64;      // partials the merge reads
 constexpr int kMergeBatch = 8;      // partials in flight per thread in the merge
+constexpr int kMergeGroup = 8;      // chunks merged by the last of each group (two levels past 8)
+constexpr int kMaxGroups = 64;      // groups merged by the last group
+constexpr int kSeqCounter = kCountersPerSeq - 1;  // a sequence's group-level arrival counter
+static_assert(kMaxGroups < kSeqCounter, "group counters and the sequence counter share a sequence's region");
 constexpr float kLazy = 2.0f;       // rescale when a row maximum grows by more (base 2)
 constexpr int kSC1 = 16;            // cache-policy bit sc1: device-coherent access
 constexpr int kNT = 2;              // cache-policy bit nt: streaming
@@ -111,8 +115,13 @@ struct Args {
     const int32_t* seq_lens;
     void* out;
     uint32_t* counters;  // counter of sequence b at b * kCountersPerSeq; zero between calls
-    float* part_o;       // [B][max_chunks][Hq][D] o / l of each chunk
-    float* part_ml;      // [B][max_chunks][Hq][2] (m, l), base-2 logits
+    // Split-KV slots: chunk c of sequence b owns slot row0(b) + c, row0(b) =
+    // b * max_chunks in chunk mode, first(b) + b in the balanced mode (first(b)
+    // = the range holding b's first tile), so slots are unique.
+    float* part_o;       // [slots][Hq][D] o / l of each chunk
+    float* part_ml;      // [slots][Hq][2] (m, l), base-2 logits
+    float* grp_o;        // [slots][Hq][D] o / l of group gi of b at slot row0(b) + gi (more than 8 chunks)
+    float* grp_ml;       // [slots][Hq][2]
     int out_f32;
     int batch, n_q_heads, max_chunks, chunk_tiles;
     int max_pages;            // 16-token pages a block-table row addresses
@@ -258,7 +267,7 @@ __device__ __forceinline__ void store2_sc1(float2v_t v, const __amdgpu_buffer_rs
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), rs, off, 0, kSC1);
 }
 
-template <int HKV>
+template <int HKV, bool SEG>
 // The scalars the prologue needs come first, as separate arguments: built
 // with -mllvm -amdgpu-kernarg-preload-count=10 they arrive in SGPRs with the
 // wave, so the sequence-length and block-table loads do not wait for a
@@ -282,9 +291,117 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
     const int jq = lane >> 4;  // MFMA k-chunk (A, B) or row quad (C)
     const int kvh = wave % HKV, par = wave / HKV;  // kv head; tiles of this parity
 
-    const int wg = xcd_remap(blockIdx.x, p_nblocks);
-    const int b = wg / p_max_chunks, chunk = wg % p_max_chunks;
-    const int t_begin = chunk * p_chunk_tiles;
+    // ---- this workgroup's piece of work: sequence b, tiles [t_begin, t_end),
+    // its chunk index and the sequence's chunk count, the slot of its chunk 0.
+    // Chunk mode (p_chunk_tiles > 0): (b, chunk) = (wg / max_chunks, wg %
+    // max_chunks), tiles chunk * chunk_tiles .. (the chunks of a sequence
+    // on one XCD).  Balanced mode (p_chunk_tiles < 0, ragged batches): the
+    // sequences' tiles laid end to end (T in all) are cut into W =
+    // max_chunks equal ranges [w T / W, (w + 1) T / W); a sequence is cut
+    // where the ranges meet it; workgroup w < W takes the piece holding its
+    // range's first tile, workgroup W + b sequence b's first piece when b
+    // starts inside a range.  So every piece has one workgroup and each
+    // workgroup one piece.
+    constexpr bool segmented = SEG;  // (the sign of p_chunk_tiles, a template parameter so chunk mode carries no scan)
+    int b, chunk, t_begin, t_lim = 0, seg_chunks = 0;
+    int64_t row0;
+    if constexpr (!segmented) {
+        const int wg = xcd_remap(blockIdx.x, p_nblocks);
+        b = wg / p_max_chunks;
+        chunk = wg % p_max_chunks;
+        t_begin = chunk * p_chunk_tiles;
+        row0 = (int64_t)b * p_max_chunks;
+    } else {
+        const int W = p_max_chunks;
+        const int bid = blockIdx.x;
+        const int w_self = bid < W ? xcd_remap(bid, W) : -1;
+        const int b_self = bid < W ? -1 : bid - W;
+        int* const seg = reinterpret_cast<int*>(smem);            // [6]: the piece found (the ring is still free)
+        long long* const red = reinterpret_cast<long long*>(smem + 64);  // [kWaves]
+        auto tiles_of = [&](int bb) -> long long {
+            const long long t = ((long long)p_seq_lens[bb] + kTile - 1) / kTile;
+            return t > 0 ? t : 0;
+        };
+        long long part = 0;
+        for (int bb = threadIdx.x; bb < a.batch; bb += 64 * kWaves) part += tiles_of(bb);
+        for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off, 64);
+        if (lane == 0) red[wave] = part;
+        if (threadIdx.x == 0) seg[0] = -1;
+        __syncthreads();
+        long long T = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) T += red[w];
+        __syncthreads();
+        // At most T ranges, so that none is empty and a sequence's chunks are
+        // numbered without gaps (range workgroups past them have none).
+        const long long Wl = (long long)W < T ? (long long)W : T;
+        if (T > (long long)kMaxChunkTiles * Wl) {
+            // The lengths outgrew the plan (a balanced plan made for fewer
+            // tokens): a range would not fit the page-id window.  Every
+            // workgroup sees the same T, so all of them write NaN into the
+            // whole output instead of a wrong result.
+            const int64_t n_out = (int64_t)a.batch * p_n_q_heads * D;
+            for (int64_t i = (int64_t)blockIdx.x * (64 * kWaves) + threadIdx.x; i < n_out;
+                 i += (int64_t)gridDim.x * (64 * kWaves)) {
+                if (a.out_f32) reinterpret_cast<float*>(a.out)[i] = __builtin_nanf("");
+                else reinterpret_cast<half_t*>(a.out)[i] = __builtin_bit_cast(half_t, (uint16_t)0x7E00);
+            }
+            return;
+        }
+        auto range_lo = [&](long long w) -> long long { return w * T / Wl; };
+        auto range_hi = [&](long long w) -> long long { return (w + 1) * T / Wl; };
+        long long carry = 0;
+        for (int b0 = 0; b0 < a.batch; b0 += 64 * kWaves) {
+            const int bb = b0 + (int)threadIdx.x;
+            const long long nb = bb < a.batch ? tiles_of(bb) : 0;
+            long long x = nb;  // inclusive scan over the wave
+            for (int off = 1; off < 64; off <<= 1) {
+                const long long y = __shfl_up(x, off, 64);
+                if (lane >= off) x += y;
+            }
+            if (lane == 63) red[wave] = x;
+            __syncthreads();
+            long long before = 0, sum = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const long long v = red[w];
+                if (w < wave) before += v;
+                sum += v;
+            }
+            const long long pb = carry + before + x - nb;  // the sequence's first tile in the laid-out order
+            if (nb > 0) {
+                long long w = -1;
+                if (w_self >= 0 && w_self < Wl) {
+                    const long long lo = range_lo(w_self);
+                    if (pb <= lo && lo < pb + nb && lo < range_hi(w_self)) w = w_self;
+                } else if (bb == b_self) {
+                    const long long f = ((pb + 1) * Wl - 1) / T;
+                    if (pb > range_lo(f) && pb < range_hi(f)) w = f;
+                }
+                if (w >= 0) {  // at most one thread of the workgroup
+                    const long long f = ((pb + 1) * Wl - 1) / T, l = ((pb + nb) * Wl - 1) / T;
+                    const long long lo = range_lo(w), hi = range_hi(w);
+                    seg[0] = bb;
+                    seg[1] = (int)((lo > pb ? lo : pb) - pb);
+                    seg[2] = (int)((hi < pb + nb ? hi : pb + nb) - pb);
+                    seg[3] = (int)(w - f);
+                    seg[4] = (int)(l - f + 1);
+                    seg[5] = (int)f;
+                }
+            }
+            carry += sum;
+            __syncthreads();
+        }
+        b = __builtin_amdgcn_readfirstlane(seg[0]);
+        if (b < 0) return;  // no piece (uniform over the workgroup)
+        t_begin = __builtin_amdgcn_readfirstlane(seg[1]);
+        t_lim = __builtin_amdgcn_readfirstlane(seg[2]);
+        chunk = __builtin_amdgcn_readfirstlane(seg[3]);
+        seg_chunks = __builtin_amdgcn_readfirstlane(seg[4]);
+        row0 = (int64_t)__builtin_amdgcn_readfirstlane(seg[5]) + b;
+        __syncthreads();  // the ring's first bytes are loaded into next
+    }
+    const int share = segmented ? -p_chunk_tiles : p_chunk_tiles;
     const int p0 = 2 * t_begin;
     const int seq_len = p_seq_lens[b];
 
@@ -309,9 +426,9 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
 
     const int n_tiles = (seq_len + kTile - 1) / kTile;
     if (t_begin >= n_tiles) return;  // uniform over the workgroup
-    const int t_end = min(t_begin + p_chunk_tiles, n_tiles);
+    const int t_end = segmented ? t_lim : min(t_begin + share, n_tiles);
     const int n_stages = t_end - t_begin;
-    const int n_chunks = (n_tiles + p_chunk_tiles - 1) / p_chunk_tiles;
+    const int n_chunks = segmented ? seg_chunks : (n_tiles + share - 1) / share;
     const int last_lp = (seq_len + kPage - 1) / kPage - 1;
 
     // ---- this wave's three loads of a slot (the same every step); each
@@ -633,71 +750,172 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
         return;
     }
 
-    // ---- split-KV: publish (o / l, m, l) with device-coherent stores; the
-    // last chunk to arrive merges every chunk of the sequence.
-    const uint32_t part_o = (uint32_t)total * 4, part_ml = (uint32_t)hq * 8;  // bytes per partial
-    const int64_t row0 = (int64_t)b * p_max_chunks;
-    {
-        const auto ro = buf_rsrc(a.part_o + (row0 + chunk) * total, part_o);
-        const auto rm = buf_rsrc(a.part_ml + (row0 + chunk) * hq * 2, part_ml);
-        for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
-            float m, l;
-            const float4_t v = chunk4(e4, m, l);
-            store4_sc1(v, ro, (uint32_t)e4 * 16);
-            if ((4 * e4) % D == 0) store2_sc1(float2v_t{m, l}, rm, (uint32_t)(4 * e4 / D) * 8);
+    if constexpr (!SEG) {
+        // Chunk mode: at most 64 chunks a sequence, merged in one level.
+        // ---- split-KV: publish (o / l, m, l) with device-coherent stores; the
+        // last chunk to arrive merges every chunk of the sequence.
+        const uint32_t part_o = (uint32_t)total * 4, part_ml = (uint32_t)hq * 8;  // bytes per partial
+        const int64_t row0 = (int64_t)b * p_max_chunks;
+        {
+            const auto ro = buf_rsrc(a.part_o + (row0 + chunk) * total, part_o);
+            const auto rm = buf_rsrc(a.part_ml + (row0 + chunk) * hq * 2, part_ml);
+            for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
+                float m, l;
+                const float4_t v = chunk4(e4, m, l);
+                store4_sc1(v, ro, (uint32_t)e4 * 16);
+                if ((4 * e4) % D == 0) store2_sc1(float2v_t{m, l}, rm, (uint32_t)(4 * e4 / D) * 8);
+            }
         }
-    }
-    wait_vmcnt<0>();
-    __syncthreads();
-    uint32_t* const ctl = reinterpret_cast<uint32_t*>(smem + 2 * HKV * L::EPI_AREA);
-    if (threadIdx.x == 0)
-        ctl[0] = arrive_last(a.counters + (int64_t)b * kCountersPerSeq, (uint32_t)n_chunks) ? 1u : 0u;
-    __syncthreads();
-    if (ctl[0] == 0) return;
+        wait_vmcnt<0>();
+        __syncthreads();
+        uint32_t* const ctl = reinterpret_cast<uint32_t*>(smem + 2 * HKV * L::EPI_AREA);
+        if (threadIdx.x == 0)
+            ctl[0] = arrive_last(a.counters + (int64_t)b * kCountersPerSeq, (uint32_t)n_chunks) ? 1u : 0u;
+        __syncthreads();
+        if (ctl[0] == 0) return;
 
-    // Merge the M = n_chunks partials, each thread a float4 of the output:
-    // o = sum_c w_c (o / l)_c / sum_c w_c with w_c = l_c 2^(m_c - m*), the
-    // partials and their (m, l) loaded together, kMergeBatch chunks at a
-    // time, m* the running maximum.  This chunk's own partial comes from LDS
-    // (the same values it published).
-    const int M = n_chunks;
-    const auto ro = buf_rsrc(a.part_o + row0 * total, part_o * (uint32_t)M);
-    const auto rm = buf_rsrc(a.part_ml + row0 * hq * 2, part_ml * (uint32_t)M);
-    for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
-        const int h = 4 * e4 / D;
-        float mstar = -INFINITY, lsum = 0.0f;
-        float4_t acc = {0, 0, 0, 0};
-        for (int c0 = 0; c0 < M; c0 += kMergeBatch) {
-            float4_t oc[kMergeBatch];
-            float2v_t ml[kMergeBatch];
-#pragma unroll
-            for (int cb = 0; cb < kMergeBatch; ++cb) {
-                const int c = min(c0 + cb, M - 1);
-                if (c != chunk) {
-                    oc[cb] = load4_sc1(ro, (uint32_t)c * part_o + (uint32_t)e4 * 16);
-                    ml[cb] = load2_sc1(rm, ((uint32_t)c * (uint32_t)hq + (uint32_t)h) * 8);
+        // Merge the M = n_chunks partials, each thread a float4 of the output:
+        // o = sum_c w_c (o / l)_c / sum_c w_c with w_c = l_c 2^(m_c - m*), the
+        // partials and their (m, l) loaded together, kMergeBatch chunks at a
+        // time, m* the running maximum.  This chunk's own partial comes from LDS
+        // (the same values it published).
+        const int M = n_chunks;
+        const auto ro = buf_rsrc(a.part_o + row0 * total, part_o * (uint32_t)M);
+        const auto rm = buf_rsrc(a.part_ml + row0 * hq * 2, part_ml * (uint32_t)M);
+        for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
+            const int h = 4 * e4 / D;
+            float mstar = -INFINITY, lsum = 0.0f;
+            float4_t acc = {0, 0, 0, 0};
+            for (int c0 = 0; c0 < M; c0 += kMergeBatch) {
+                float4_t oc[kMergeBatch];
+                float2v_t ml[kMergeBatch];
+    #pragma unroll
+                for (int cb = 0; cb < kMergeBatch; ++cb) {
+                    const int c = min(c0 + cb, M - 1);
+                    if (c != chunk) {
+                        oc[cb] = load4_sc1(ro, (uint32_t)c * part_o + (uint32_t)e4 * 16);
+                        ml[cb] = load2_sc1(rm, ((uint32_t)c * (uint32_t)hq + (uint32_t)h) * 8);
+                    } else {
+                        float m, l;
+                        oc[cb] = chunk4(e4, m, l);
+                        ml[cb] = float2v_t{m, l};
+                    }
+                }
+                // past M: a repeat of partial M - 1 with weight 0
+                float mb = mstar;
+    #pragma unroll
+                for (int cb = 0; cb < kMergeBatch; ++cb) mb = fmaxf(mb, ml[cb][0]);
+                const float r = __builtin_amdgcn_exp2f(mstar - mb);  // 0 on the first batch
+                acc *= r;
+                lsum *= r;
+    #pragma unroll
+                for (int cb = 0; cb < kMergeBatch; ++cb) {
+                    const float w = c0 + cb < M ? ml[cb][1] * __builtin_amdgcn_exp2f(ml[cb][0] - mb) : 0.0f;
+                    acc += oc[cb] * w;
+                    lsum += w;
+                }
+                mstar = mb;
+            }
+            store_out4(e4, acc * (1.0f / lsum));
+        }
+    } else {
+        // Balanced mode: up to 8 x 64 chunks a sequence, two levels.
+        // ---- split-KV: publish (o / l, m, l) with device-coherent stores; the
+        // last chunk of each group of kMergeGroup chunks to arrive merges the
+        // group; with more than one group, the group partials go out the same
+        // way and the last group to arrive merges them (two levels, so no
+        // workgroup reads more than kMergeGroup chunk partials or kMaxGroups
+        // group partials).
+        const uint32_t part_o = (uint32_t)total * 4, part_ml = (uint32_t)hq * 8;  // bytes per partial
+        {
+            const auto ro = buf_rsrc(a.part_o + (row0 + chunk) * total, part_o);
+            const auto rm = buf_rsrc(a.part_ml + (row0 + chunk) * hq * 2, part_ml);
+            for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
+                float m, l;
+                const float4_t v = chunk4(e4, m, l);
+                store4_sc1(v, ro, (uint32_t)e4 * 16);
+                if ((4 * e4) % D == 0) store2_sc1(float2v_t{m, l}, rm, (uint32_t)(4 * e4 / D) * 8);
+            }
+        }
+        wait_vmcnt<0>();
+        __syncthreads();
+        uint32_t* const ctl = reinterpret_cast<uint32_t*>(smem + 2 * HKV * L::EPI_AREA);
+        uint32_t* const seq_ctr = a.counters + (int64_t)b * kCountersPerSeq;
+        // Arrival at a counter (the protocol of arrive_last): true in the
+        // workgroup that completes `expect` arrivals.
+        auto arrive = [&](uint32_t* counter, int expect) __attribute__((always_inline)) -> bool {
+            if (threadIdx.x == 0) ctl[0] = arrive_last(counter, (uint32_t)expect) ? 1u : 0u;
+            __syncthreads();
+            const bool last = ctl[0] != 0;
+            __syncthreads();
+            return last;
+        };
+        // Merge M partials (o / l at po, (m, l) at pm; partial `own` from LDS)
+        // into the output, or into the group partial at (wo, wm): each thread
+        // float4s of it, o = sum_c w_c (o / l)_c / sum_c w_c with
+        // w_c = l_c 2^(m_c - m*), kMergeBatch partials and their (m, l) in
+        // flight, m* the running maximum.
+        auto merge = [&](const float* po, const float* pm, int M, int own, bool to_out, float* wo,
+                         float* wm) __attribute__((always_inline)) {
+            const auto ro = buf_rsrc(po, part_o * (uint32_t)M);
+            const auto rm = buf_rsrc(pm, part_ml * (uint32_t)M);
+            const auto wro = buf_rsrc(wo, to_out ? 0u : part_o);
+            const auto wrm = buf_rsrc(wm, to_out ? 0u : part_ml);
+            for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
+                const int h = 4 * e4 / D;
+                float mstar = -INFINITY, lsum = 0.0f;
+                float4_t acc = {0, 0, 0, 0};
+                for (int c0 = 0; c0 < M; c0 += kMergeBatch) {
+                    float4_t oc[kMergeBatch];
+                    float2v_t ml[kMergeBatch];
+    #pragma unroll
+                    for (int cb = 0; cb < kMergeBatch; ++cb) {
+                        const int c = min(c0 + cb, M - 1);
+                        if (c != own) {
+                            oc[cb] = load4_sc1(ro, (uint32_t)c * part_o + (uint32_t)e4 * 16);
+                            ml[cb] = load2_sc1(rm, ((uint32_t)c * (uint32_t)hq + (uint32_t)h) * 8);
+                        } else {
+                            float m, l;
+                            oc[cb] = chunk4(e4, m, l);
+                            ml[cb] = float2v_t{m, l};
+                        }
+                    }
+                    // past M: a repeat of partial M - 1 with weight 0
+                    float mb = mstar;
+    #pragma unroll
+                    for (int cb = 0; cb < kMergeBatch; ++cb) mb = fmaxf(mb, ml[cb][0]);
+                    const float r = __builtin_amdgcn_exp2f(mstar - mb);  // 0 on the first batch
+                    acc *= r;
+                    lsum *= r;
+    #pragma unroll
+                    for (int cb = 0; cb < kMergeBatch; ++cb) {
+                        const float w = c0 + cb < M ? ml[cb][1] * __builtin_amdgcn_exp2f(ml[cb][0] - mb) : 0.0f;
+                        acc += oc[cb] * w;
+                        lsum += w;
+                    }
+                    mstar = mb;
+                }
+                const float4_t res = acc * (1.0f / lsum);
+                if (to_out) {
+                    store_out4(e4, res);
                 } else {
-                    float m, l;
-                    oc[cb] = chunk4(e4, m, l);
-                    ml[cb] = float2v_t{m, l};
+                    store4_sc1(res, wro, (uint32_t)e4 * 16);
+                    if ((4 * e4) % D == 0) store2_sc1(float2v_t{mstar, lsum}, wrm, (uint32_t)h * 8);
                 }
             }
-            // past M: a repeat of partial M - 1 with weight 0
-            float mb = mstar;
-#pragma unroll
-            for (int cb = 0; cb < kMergeBatch; ++cb) mb = fmaxf(mb, ml[cb][0]);
-            const float r = __builtin_amdgcn_exp2f(mstar - mb);  // 0 on the first batch
-            acc *= r;
-            lsum *= r;
-#pragma unroll
-            for (int cb = 0; cb < kMergeBatch; ++cb) {
-                const float w = c0 + cb < M ? ml[cb][1] * __builtin_amdgcn_exp2f(ml[cb][0] - mb) : 0.0f;
-                acc += oc[cb] * w;
-                lsum += w;
-            }
-            mstar = mb;
-        }
-        store_out4(e4, acc * (1.0f / lsum));
+        };
+        const int grp = chunk / kMergeGroup;
+        const int n_groups = (n_chunks + kMergeGroup - 1) / kMergeGroup;
+        const int members = min(kMergeGroup, n_chunks - grp * kMergeGroup);
+        if (!arrive(seq_ctr + grp, members)) return;
+        const int64_t c0row = row0 + grp * kMergeGroup;
+        merge(a.part_o + c0row * total, a.part_ml + c0row * hq * 2, members, chunk - grp * kMergeGroup, n_groups == 1,
+              a.grp_o + (row0 + grp) * total, a.grp_ml + (row0 + grp) * hq * 2);
+        if (n_groups == 1) return;
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (!arrive(seq_ctr + kSeqCounter, n_groups)) return;
+        merge(a.grp_o + row0 * total, a.grp_ml + row0 * hq * 2, n_groups, -1, true, a.grp_o, a.grp_ml);
     }
 }
 
@@ -714,14 +932,14 @@ int stream_lds_bytes() {
     return L::LDS_MAIN > epi ? L::LDS_MAIN : epi;
 }
 
-template <int HKV>
+template <int HKV, bool SEG>
 int launch_stream(dim3 grid, hipStream_t s, const st::Args& a) {
     const int lds = stream_lds_bytes<HKV>();
     if (lds > kMaxLdsBytes) return kInvalidArgument;
     static std::atomic<uint64_t> lds_raised{0};
-    if (allow_full_lds(reinterpret_cast<const void*>(&st::int4_decode_stream_kernel<HKV>), lds_raised) != kOk)
+    if (allow_full_lds(reinterpret_cast<const void*>(&st::int4_decode_stream_kernel<HKV, SEG>), lds_raised) != kOk)
         return kLaunchError;
-    hipLaunchKernelGGL((st::int4_decode_stream_kernel<HKV>), grid, dim3(64 * st::kWaves), lds, s, a.seq_lens, a.block_table, a.q,
+    hipLaunchKernelGGL((st::int4_decode_stream_kernel<HKV, SEG>), grid, dim3(64 * st::kWaves), lds, s, a.seq_lens, a.block_table, a.q,
                        a.max_chunks, a.chunk_tiles, a.bt_cols, a.max_pages, a.page_shift, a.n_q_heads, (int)grid.x, a);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchError;
 }
@@ -734,9 +952,28 @@ bool stream_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t head_di
     return head_dim == 128 && num_kv_heads == 8 && num_q_heads == 4 * num_kv_heads;
 }
 
+// Split-KV workspace: [counters][chunk partials o][chunk (m, l)] and, when a
+// sequence can have more than kMergeGroup chunks, [group partials o][group
+// (m, l)], `slots` of each (B x max_chunks in chunk mode, W + B in the
+// balanced mode).
+struct StreamWorkspace {
+    int64_t part_o, part_ml, grp_o, grp_ml, total;
+};
+static StreamWorkspace stream_workspace(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t slots,
+                                        bool two_level) {
+    auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+    StreamWorkspace w;
+    w.part_o = counter_region_bytes(batch);
+    w.part_ml = w.part_o + up(slots * num_q_heads * head_dim * 4);
+    w.grp_o = w.part_ml + up(slots * num_q_heads * 2 * 4);
+    const int64_t g = two_level ? slots : 0;
+    w.grp_ml = w.grp_o + up(g * num_q_heads * head_dim * 4);
+    w.total = w.grp_ml + g * num_q_heads * 2 * 4;
+    return w;
+}
+
 int64_t stream_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t max_chunks) {
-    const int64_t o = batch * max_chunks * num_q_heads * head_dim * 4;
-    return counter_region_bytes(batch) + (o + 255) / 256 * 256 + batch * max_chunks * num_q_heads * 2 * 4;
+    return stream_workspace(batch, num_q_heads, head_dim, batch * max_chunks, false).total;  // chunk mode: one level
 }
 
 int stream_launch(const void* query, const void* k_data, const void* v_data, const void* k_scale, const void* v_scale,
@@ -745,10 +982,15 @@ int stream_launch(const void* query, const void* k_data, const void* v_data, con
                   int64_t num_kv_heads, int64_t head_dim, int64_t max_pages, int64_t bt_cols, int32_t page_shift,
                   float softmax_scale, int32_t chunk_tiles, int32_t max_chunks, void* stream) {
     if (!stream_supported(num_q_heads, num_kv_heads, head_dim)) return kInvalidArgument;
-    if (chunk_tiles <= 0 || chunk_tiles > st::kMaxChunkTiles || max_chunks <= 0 || max_chunks > st::kMaxChunks)
-        return kInvalidArgument;
-    if ((int64_t)chunk_tiles * max_chunks * 2 < max_pages) return kInvalidArgument;  // the grid covers every page
-    const int64_t nblocks = batch * (int64_t)max_chunks;
+    // chunk_tiles > 0: chunk mode, batch x max_chunks workgroups; < 0: the
+    // balanced mode, max_chunks ranges of at most -chunk_tiles tiles plus
+    // one sequence-start workgroup per sequence.
+    const bool balanced = chunk_tiles < 0;
+    const int64_t share = balanced ? -(int64_t)chunk_tiles : chunk_tiles;
+    if (share <= 0 || share > st::kMaxChunkTiles || max_chunks <= 0) return kInvalidArgument;
+    if (balanced ? max_chunks > st::kMergeGroup * st::kMaxGroups : max_chunks > st::kMaxChunks) return kInvalidArgument;
+    if (!balanced && share * max_chunks * 2 < max_pages) return kInvalidArgument;  // the grid covers every page
+    const int64_t nblocks = balanced ? max_chunks + batch : batch * (int64_t)max_chunks;
     if (nblocks > 0x7FFFFFFF) return kInvalidArgument;
     st::Args a;
     a.q = (const half_t*)query;
@@ -769,17 +1011,21 @@ int stream_launch(const void* query, const void* k_data, const void* v_data, con
     a.chunk_tiles = chunk_tiles;
     a.log2_scale = softmax_scale * 1.4426950408889634f;
     a.counters = nullptr;
-    a.part_o = a.part_ml = nullptr;
-    if (max_chunks > 1) {
-        const int64_t need = stream_workspace_bytes(batch, num_q_heads, head_dim, max_chunks);
-        if (workspace == nullptr || workspace_bytes_avail < need) return kWorkspaceTooSmall;
+    a.part_o = a.part_ml = a.grp_o = a.grp_ml = nullptr;
+    if (max_chunks > 1) {  // (one balanced range: every piece is a whole sequence)
+        const StreamWorkspace w = balanced ? stream_workspace(batch, num_q_heads, head_dim, max_chunks + batch,
+                                                              max_chunks > st::kMergeGroup)
+                                           : stream_workspace(batch, num_q_heads, head_dim, batch * max_chunks, false);
+        if (workspace == nullptr || workspace_bytes_avail < w.total) return kWorkspaceTooSmall;
         uint8_t* const ws = (uint8_t*)workspace;
-        const int64_t o = batch * max_chunks * num_q_heads * head_dim * 4;
         a.counters = (uint32_t*)ws;
-        a.part_o = (float*)(ws + counter_region_bytes(batch));
-        a.part_ml = (float*)(ws + counter_region_bytes(batch) + (o + 255) / 256 * 256);
+        a.part_o = (float*)(ws + w.part_o);
+        a.part_ml = (float*)(ws + w.part_ml);
+        a.grp_o = (float*)(ws + w.grp_o);
+        a.grp_ml = (float*)(ws + w.grp_ml);
     }
-    return launch_stream<8>(dim3((unsigned)nblocks), (hipStream_t)stream, a);
+    if (balanced) return launch_stream<8, true>(dim3((unsigned)nblocks), (hipStream_t)stream, a);
+    return launch_stream<8, false>(dim3((unsigned)nblocks), (hipStream_t)stream, a);
 }
 
 }  // namespace iris
