@@ -69,6 +69,21 @@ def test_config_decode_matches_eager(device, cfg, kernel):
     log(f"decode: config {cfg} {kernel} max-abs err fp32 {e32:.2e} fp16 {e16:.2e}")
 
 
+@pytest.mark.parametrize("cfg", [2, 3])
+def test_page_kernel_forced_matches_eager(device, cfg, monkeypatch):
+    # At the streaming kernel's shape a 16-wave plan runs the streaming
+    # kernel (chunk mode at cfg2, balanced mode at cfg3);
+    # IRIS_DECODE_KERNEL=pages keeps the page-streaming kernel, which must
+    # hold the same contract.
+    monkeypatch.setenv("IRIS_DECODE_KERNEL", "pages")
+    case, cpu, gpu = prepared(cfg, device)
+    if cfg not in _WANT:
+        _WANT[cfg] = eager_fp32(case, cpu)
+    got = run(case, gpu, device, torch.float32, waves_per_block=16)
+    e = assert_attention_close(got, _WANT[cfg], f"cfg{cfg} page kernel forced")
+    log(f"decode: config {cfg} page kernel forced max-abs err {e:.2e}")
+
+
 @pytest.mark.parametrize("kernel", list(KERNELS))
 def test_config5_long_context_against_float64(device, kernel):
     # L = 131072 per sequence: the float64 C checker (the torch one would
