@@ -13,7 +13,8 @@
 // 512 of V codes and 64 of each scale tensor, four small regions.  Read by
 // one wave each they stream poorly, so a workgroup of 16 waves owns
 // (sequence, chunk of 32-token tiles) and streams 16 tiles (32 pages) a step
-// through a ring of three 36 KiB LDS slots, two in flight:
+// through a ring of two 36 KiB LDS slots, one in flight while the other is
+// computed (deeper queues measured slower):
 // * slot s holds the K codes, V codes, K scales and V scales of tiles
 //   16 s .. 16 s + 15 of the chunk; every load moves 1 KiB straight into LDS
 //   (wave w: K and V of tile 16 s + w, one load each covering both pages;
@@ -50,8 +51,8 @@ namespace mq {
 
 constexpr int kTile = 32;
 constexpr int kWaves = 16;
-constexpr int kSlots = 3;           // ring slots
-constexpr int kAhead = 2;           // slots in flight
+constexpr int kSlots = 2;           // ring slots
+constexpr int kAhead = 1;           // slots in flight (two or three measured 0.8-2 us slower at cfg4)
 constexpr int kJobs = 3;            // loads per wave per slot
 constexpr int kMaxChunkTiles = 128;  // the page-id table holds 2 * 128 entries
 constexpr int kMaxChunks = 64;
@@ -300,7 +301,6 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
         }
     };
     issue(0);
-    if (n_steps > 1) issue(1);
 
     // ---- q operands (in the order of k_operand; high-nibble dims / 16) and
     // the accumulator start that removes the +8 of the K codes: C row (token)
@@ -435,14 +435,14 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
         }
     };
 
-    // ---- the pipeline.  Step s: wait for this wave's loads of slot s (slot
-    // s + 1 stays in flight); the barrier makes every wave's loads of slot s
-    // visible and frees slot s - 1, which receives slot s + 2.
+    // ---- the pipeline.  Step s: wait for this wave's loads of slot s; the
+    // barrier makes every wave's loads of slot s visible and frees slot
+    // s - 1, which receives slot s + 1 while slot s is computed.
+    static_assert(kAhead == 1 && kSlots == 2, "one slot computed, one in flight");
     for (int s = 0; s < n_steps; ++s) {
-        if (s + 1 < n_steps) wait_vmcnt<(kAhead - 1) * kJobs>();
-        else wait_vmcnt<0>();
+        wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
-        if (s + 2 < n_steps) issue(s + 2);
+        if (s + 1 < n_steps) issue(s + 1);
         const int tile = t_begin + kWaves * s + wave;
         if (tile < t_end) compute(tile, lds_addr(smem) + (uint32_t)((s % kSlots) * SLOT));
     }
