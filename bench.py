@@ -80,7 +80,7 @@ def decode_kernel_name(plan, group: int, n_kv: int, d: int, batch: int, max_page
     if (plan[2] == 16 and plan[0] > 0 and plan[1] <= 64 and d == 128 and n_kv == 8 and group == 4
             and os.environ.get("IRIS_DECODE_KERNEL") != "pages"):
         # (rocprofv3 prints this kernel mangled: _Float16 in its signature)
-        return "_ZN4iris2st25int4_decode_stream_kernelILi8EEEvPKiS3_PKDF16_iiiiiiiNS0_4ArgsE"
+        return "_ZN4iris2st25int4_decode_stream_kernelILi8ELb0EEEvPKiS3_PKDF16_iiiiiiiNS0_4ArgsE"
     if plan[2] == 16 and n_kv == 1 and d == 64 and group <= 16 and os.environ.get("IRIS_DECODE_KERNEL") != "pages":
         return "_ZN4iris2mq22int4_decode_mqa_kernelEPKiS2_PKDF16_iiiiiiNS0_4ArgsE"  # (printed mangled)
     if plan[2] == 16:
