@@ -49,15 +49,16 @@ def noalloc_call(q, cache, bt, sl, out, scale, plan):
         ctypes.c_float(scale), chunk_tiles, max_chunks, nw, _lib.raw_stream(q.device))
 
 
-def one_call(device, batch, max_pages, max_len, tokens_per_split, seed):
-    hq, hkv, d = 32, 8, 128
+def one_call(device, batch, max_pages, max_len, tokens_per_split, seed, hq=32, hkv=8, d=128, waves=0):
     gen = torch.Generator().manual_seed(seed)
     q, cache, bt, sl = make_case(batch, hq, hkv, d, max_pages, max_len, gen)
     q, bt, sl = (t.to(device) for t in (q, bt, sl))
     cache = tuple(t.to(device) for t in cache)
-    plan = decode_plan(batch, hq, hkv, d, max_pages, int(sl.sum()), int(sl.max()), tokens_per_split, 0)
+    plan = decode_plan(batch, hq, hkv, d, max_pages, int(sl.sum()), int(sl.max()), tokens_per_split, waves)
     assert plan[1] > 1 and 0 < plan[3] <= SCRATCH_BYTES, plan
-    log(f"no-alloc: batch={batch} max_len={max_len} plan={plan}")
+    if waves:
+        assert plan[2] == waves, plan
+    log(f"no-alloc: batch={batch} hq={hq} hkv={hkv} d={d} max_len={max_len} plan={plan}")
     scale = d ** -0.5
     want = torch.empty(q.shape, dtype=torch.float16, device=device)
     fa._launch_decode(q, *cache, bt, sl, want, scale, plan)
@@ -72,6 +73,17 @@ def one_call(device, batch, max_pages, max_len, tokens_per_split, seed):
 def test_noalloc_matches_workspace_entry_two_calls(device):
     one_call(device, batch=12, max_pages=96, max_len=1536, tokens_per_split=256, seed=11)
     one_call(device, batch=5, max_pages=48, max_len=700, tokens_per_split=128, seed=12)
+
+
+def test_noalloc_streaming_kernels_two_calls(device):
+    """16-wave plans: the streaming kernel (Hkv 8, D 128, ragged lengths) and
+    the MQA kernel (one kv head, D 64), each larger call then smaller."""
+    one_call(device, batch=8, max_pages=256, max_len=4096, tokens_per_split=0, seed=21, waves=16)
+    one_call(device, batch=3, max_pages=128, max_len=2048, tokens_per_split=0, seed=22, waves=16)
+    one_call(device, batch=16, max_pages=512, max_len=8192, tokens_per_split=0, seed=23, hq=16, hkv=1, d=64,
+             waves=16)
+    one_call(device, batch=6, max_pages=256, max_len=4096, tokens_per_split=0, seed=24, hq=16, hkv=1, d=64,
+             waves=16)
 
 
 def test_noalloc_rejects_plan_beyond_scratch(device):
