@@ -10,22 +10,21 @@
 // Streaming
 // ---------
 // A 16-token page of one kv head at head_dim 64 is 512 bytes of K codes,
-// 512 of V codes and 64 of each scale tensor, four small regions.  Read by
-// one wave each they stream poorly, so a workgroup of 16 waves owns
-// (sequence, chunk of 32-token tiles) and streams 16 tiles (32 pages) a step
-// through a ring of two 36 KiB LDS slots, one in flight while the other is
-// computed (deeper queues measured slower):
-// * slot s holds the K codes, V codes, K scales and V scales of tiles
-//   16 s .. 16 s + 15 of the chunk; every load moves 1 KiB straight into LDS
-//   (wave w: K and V of tile 16 s + w, one load each covering both pages;
-//   waves 0-3: the scales of 8 tiles of one tensor each; waves 4-15 an empty
-//   load, so every wave has three loads of every slot in flight);
-// * the chunk's page ids sit in an LDS table, so any lane can look up any
-//   page (the scale loads gather 16 pages a load).
+// 512 of V codes and 64 of each scale tensor, four small regions.  A
+// workgroup of 16 waves owns (sequence, chunk of 32-token tiles); wave w
+// streams tiles w, w + 16, w + 32, ... of the chunk through a ring of its
+// own in LDS, with no workgroup barrier between tiles:
+// * a slot (one tile, 2304 bytes) is filled by three loads straight into
+//   LDS: K and V codes (one 16-byte-a-lane load each, covering both pages)
+//   and the scales (one dword a lane: K of both pages, then V);
+// * one tile is in flight while the previous one is computed (a barrier a
+//   step across the 16 waves, with shared scale loads, measured 23.4 us
+//   against 21.5 us at configuration 4; deeper rings measured slower);
+// * the chunk's page ids sit in an LDS table, read before the loop.
 //
-// Compute: one tile a wave a step
-// -------------------------------
-// Wave w computes tile 16 s + w of step s, a whole 32-token tile, with the
+// Compute: one tile a wave at a time
+// -----------------------------------
+// Wave w computes its tiles one at a time, a whole 32-token tile each, with the
 // 16 query heads as the MFMA columns (v_mfma_f32_16x16x32_f16):
 // * QK: S^T[t][h] = sum_g ks[t][g] * sum_{d in g} (K codes of 16 tokens,
 //   one 32-dim group: A) x (q, B); the K codes enter as exact fp16
@@ -51,10 +50,11 @@ namespace mq {
 
 constexpr int kTile = 32;
 constexpr int kWaves = 16;
-constexpr int kSlots = 2;           // ring slots
-constexpr int kAhead = 1;           // slots in flight (two or three measured 0.8-2 us slower at cfg4)
-constexpr int kJobs = 3;            // loads per wave per slot
-constexpr int kMaxChunkTiles = 128;  // the page-id table holds 2 * 128 entries
+// A wave's ring slots: kRing - 1 tiles in flight while one is computed
+// (three or four slots measured 1.3-2.4 us slower at configuration 4).
+constexpr int kRing = 2;
+constexpr int kJobs = 3;              // loads per wave per tile (K codes, V codes, both scales)
+constexpr int kMaxChunkTiles = 128;   // the page-id table holds 2 * 128 entries
 constexpr int kMaxChunks = 64;
 constexpr int kMergeBatch = 8;
 constexpr int kSC1 = 16;  // cache-policy bit sc1: device-coherent access
@@ -63,11 +63,11 @@ constexpr int kNT = 2;    // cache-policy bit nt: streaming
 constexpr int D = 64, G = 2;
 constexpr uint32_t KPAGE = 16 * 32;  // code bytes of a page (per tensor)
 constexpr uint32_t SPAGE = 16 * 4;   // scale bytes of a page (per tensor)
-// Slot: [K: 16 tiles x 1 KiB][V: 16 x 1 KiB][KS: 16 x 128 B][VS: 16 x 128 B]
-constexpr int K_OFF = 0, V_OFF = 16 * 1024, KS_OFF = 32 * 1024, VS_OFF = 34 * 1024, SLOT = 36 * 1024;
-constexpr int PID_OFF = kSlots * SLOT;       // page-id table: 2 * kMaxChunkTiles int32
-constexpr int SINK_OFF = PID_OFF + 4 * 2 * kMaxChunkTiles;
-constexpr int LDS_BYTES = SINK_OFF + 1024;
+// A wave's slot (one tile): [K codes 1 KiB][V codes 1 KiB][K scales 128 B]
+// [V scales 128 B]; wave w's ring is slots w * kRing .. w * kRing + kRing - 1.
+constexpr int K_OFF = 0, V_OFF = 1024, KS_OFF = 2048, VS_OFF = 2048 + 128, SLOT = 2304;
+constexpr int PID_OFF = kWaves * kRing * SLOT;  // page-id table: 2 * kMaxChunkTiles int32
+constexpr int LDS_BYTES = PID_OFF + 4 * 2 * kMaxChunkTiles;
 // Epilogue (over the ring once the loop is done): per wave [m 16][l 16]
 // [o 16 heads x 65 (64 dims, padded)] fp32.
 constexpr int EPI_ROW = 65;
@@ -259,48 +259,42 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
     __syncthreads();
     const uint32_t tab = lds_addr(ptab);
 
-    // ---- this wave's loads of a slot.  Per-lane parts of the addresses:
-    // * K of tile w, 1 KiB at K_OFF + 1024 w: position P = 16 (2 e + g) + m
-    //   holds token m of page e, dims of group g (16 bytes), so lane
-    //   (m, k-chunk c) reads dword c of position 16 (2 e + g) + m;
-    // * V of tile w at V_OFF + 1024 w: position 2 tau + p holds chunk
-    //   p ^ (tau & 1) of token tau (tau = 16 e + row), so the transposed
-    //   reads of a group hit every bank once;
-    // * scales: position (2 w' + e) 4 + j of a 1 KiB block (8 tiles w') holds
-    //   bytes 16 j .. of page e's 64 (four tokens' two groups each).
+    // ---- this wave's loads of its tile number s (chunk-relative tile
+    // 16 s + wave) into its ring slot s % kRing.  Per-lane parts:
+    // * K, 1 KiB at K_OFF: position P = 16 (2 e + g) + m holds token m of
+    //   page e, dims of group g (16 bytes), so lane (m, k-chunk c) reads
+    //   dword c of position 16 (2 e + g) + m;
+    // * V, 1 KiB at V_OFF: position 2 tau + p holds chunk p ^ (tau & 1) of
+    //   token tau (tau = 16 e + row), so the transposed reads of a group hit
+    //   every bank once;
+    // * scales, 256 B at KS_OFF: the 64 bytes of K scales of pages 0 and 1,
+    //   then those of V, one dword a lane.
     const uint32_t k_lane = (uint32_t)((lane & 15) * 32 + ((lane >> 4) & 1) * 16);
     const int v_tau = lane >> 1;
     const uint32_t v_lane = (uint32_t)((v_tau & 15) * 32 + 16 * ((lane & 1) ^ (v_tau & 1)));
-    const uint32_t s_lane = (uint32_t)(16 * (lane & 3));
-    const bool s_job = wave < 4;
-    const bool s_is_v = wave >= 2;
-    const int s_q = wave & 1;
-    const uint8_t* const s_base = s_is_v ? a.v_scale : a.k_scale;
+    const uint32_t s_lane = (uint32_t)(4 * (lane & 15));
+    const uint8_t* const s_base = lane >= 32 ? a.v_scale : a.k_scale;
+    uint8_t* const ring = smem + wave * kRing * SLOT;
 
     auto issue = [&](int s) __attribute__((always_inline)) {
-        uint8_t* const dst = smem + (s % kSlots) * SLOT;
-        const int t = kWaves * s + wave;  // chunk-relative tile of this wave
+        uint8_t* const dst = ring + (s % kRing) * SLOT;
+        const int t = kWaves * s + wave;  // chunk-relative tile
         const int pa = __builtin_amdgcn_readfirstlane(lds_i32(tab + 4 * min(2 * t, jlim)));
         const int pb = __builtin_amdgcn_readfirstlane(lds_i32(tab + 4 * min(2 * t + 1, jlim)));
         const uint64_t pg = (uint64_t)(uint32_t)((lane >> 5) ? pb : pa);  // K and V: lanes 32-63 read page e = 1
+        const uint64_t ps = (uint64_t)(uint32_t)(((lane >> 4) & 1) ? pb : pa);
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.k_data + pg * KPAGE + k_lane),
-                                         (IRIS_LDS void*)(dst + K_OFF + 1024 * wave), 16, 0, kNT);
+                                         (IRIS_LDS void*)(dst + K_OFF), 16, 0, kNT);
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.v_data + pg * KPAGE + v_lane),
-                                         (IRIS_LDS void*)(dst + V_OFF + 1024 * wave), 16, 0, kNT);
-        if (s_job) {
-            const int tl = kWaves * s + 8 * s_q + (lane >> 3);
-            const uint32_t ps = (uint32_t)lds_i32(tab + 4 * min(2 * tl + ((lane >> 2) & 1), jlim));
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(s_base + (uint64_t)ps * SPAGE + s_lane),
-                                             (IRIS_LDS void*)(dst + (s_is_v ? VS_OFF : KS_OFF) + 1024 * s_q), 16, 0,
-                                             kNT);
-        } else {
-            // an empty load (zero-size descriptor: no memory access), so every
-            // wave has kJobs loads of the slot in flight
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(buf_rsrc(a.k_data, 0u), (IRIS_LDS void*)(smem + SINK_OFF), 16,
-                                                     0, 0, 0, 0);
-        }
+                                         (IRIS_LDS void*)(dst + V_OFF), 16, 0, kNT);
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(s_base + ps * SPAGE + s_lane),
+                                         (IRIS_LDS void*)(dst + KS_OFF), 4, 0, kNT);
     };
-    issue(0);
+    // This wave's tiles: 16 s + wave < n_ct.
+    const int n_my = n_ct > wave ? (n_ct - wave + kWaves - 1) / kWaves : 0;
+#pragma unroll
+    for (int s = 0; s < kRing - 1; ++s)
+        if (s < n_my) issue(s);
 
     // ---- q operands (in the order of k_operand; high-nibble dims / 16) and
     // the accumulator start that removes the +8 of the K codes: C row (token)
@@ -321,16 +315,16 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
     }
 
     // ---- per-lane LDS offsets within a slot (this wave's tile)
-    const uint32_t k_rd = (uint32_t)(K_OFF + 1024 * wave + 16 * n + 4 * jq);
-    const uint32_t ks_rd = (uint32_t)(KS_OFF + 128 * wave + 16 * jq);
-    const uint32_t vs_rd = (uint32_t)(VS_OFF + 128 * wave + 16 * jq);
+    const uint32_t k_rd = (uint32_t)(K_OFF + 16 * n + 4 * jq);
+    const uint32_t ks_rd = (uint32_t)(KS_OFF + 16 * jq);
+    const uint32_t vs_rd = (uint32_t)(VS_OFF + 16 * jq);
     // Transposed V reads: lane (n, jq) supplies the 8-byte half (n & 1) of
     // token tr_tok's chunk of the group; after the 8 x 8 byte transpose it
     // holds byte column n of tokens 16 (k' >> 2) + 4 jq + (k' & 3), k' the
     // byte index (the rows of its S^T column).
     const int trk = n >> 1;
     const int tr_tok = 4 * jq + (trk & 3) + 16 * (trk >> 2);
-    const uint32_t tr0 = (uint32_t)(V_OFF + 1024 * wave + tr_tok * 32 + 8 * (n & 1) + ((trk & 1) << 4));
+    const uint32_t tr0 = (uint32_t)(V_OFF + tr_tok * 32 + 8 * (n & 1) + ((trk & 1) << 4));
     const uint32_t tr1 = tr0 ^ 16u;
 
     const float c24 = a.log2_scale * 16777216.0f;  // MFMA units -> base-2 logits
@@ -435,16 +429,25 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
         }
     };
 
-    // ---- the pipeline.  Step s: wait for this wave's loads of slot s; the
-    // barrier makes every wave's loads of slot s visible and frees slot
-    // s - 1, which receives slot s + 1 while slot s is computed.
-    static_assert(kAhead == 1 && kSlots == 2, "one slot computed, one in flight");
-    for (int s = 0; s < n_steps; ++s) {
-        wait_vmcnt<0>();
-        __builtin_amdgcn_s_barrier();
-        if (s + 1 < n_steps) issue(s + 1);
-        const int tile = t_begin + kWaves * s + wave;
-        if (tile < t_end) compute(tile, lds_addr(smem) + (uint32_t)((s % kSlots) * SLOT));
+    // ---- the pipeline, per wave (no workgroup barrier): tile s is computed
+    // once this wave's loads of it have landed (vmcnt counts in order), with
+    // tiles s + 1 .. s + kRing - 1 in flight; slot (s - 1) % kRing, read to
+    // registers by tile s - 1, receives tile s + kRing - 1 first.
+    static_assert(kRing >= 2 && kRing <= 4, "ring depth");
+    const uint32_t ring_addr = lds_addr(ring);
+    for (int s = 0; s < n_my; ++s) {
+        const int ahead = min(n_my - 1 - s, kRing - 1);  // tiles in flight behind tile s
+        if (ahead == kRing - 1) {
+            issue(s + kRing - 1);
+            wait_vmcnt<(kRing - 1) * kJobs>();
+        } else if (kRing > 3 && ahead == 2) {
+            wait_vmcnt<2 * kJobs>();
+        } else if (ahead == 1) {
+            wait_vmcnt<kJobs>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        compute(t_begin + kWaves * s + wave, ring_addr + (uint32_t)((s % kRing) * SLOT));
     }
     wait_vmcnt<0>();
     __syncthreads();
