@@ -204,12 +204,18 @@ def test_balanced_split_ragged_batches(device, case):
         assert_attention_close(out, want, f"{case} call {i}")
 
 
-def test_stale_balanced_plan_writes_nan(device):
+@pytest.mark.parametrize("kernel", ["stream", "pages"])
+def test_stale_balanced_plan_writes_nan(device, kernel, monkeypatch):
     # A balanced plan made for short ragged lengths, launched (through the
     # C ABI's launch path) with lengths whose tiles exceed what its ranges
     # can cover: every output element is NaN, not a silently truncated
-    # result, and the workspace stays usable for the next correct call.
+    # result, and the workspace stays usable for the next correct call.  At
+    # this shape the streaming kernel's balanced mode runs the plan, or the
+    # page-streaming kernel with IRIS_DECODE_KERNEL=pages.
     from iris_kernel import fused_attention as fa
+
+    if kernel == "pages":
+        monkeypatch.setenv("IRIS_DECODE_KERNEL", "pages")
 
     case, cpu, gpu = prepared(2, device)
     q, bt, full = to(device, case.query, case.block_table, case.seq_lens)
