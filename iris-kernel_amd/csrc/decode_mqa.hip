@@ -20,7 +20,9 @@
 // * one tile is in flight while the previous one is computed (a barrier a
 //   step across the 16 waves, with shared scale loads, measured 23.4 us
 //   against 21.5 us at configuration 4; deeper rings measured slower);
-// * the chunk's page ids sit in an LDS table, read before the loop.
+// * a wave's page ids sit in 16 lanes of one register (read with
+//   v_readlane: an LDS table measured 1 us slower, its reads on every
+//   tile's load path).
 //
 // Compute: one tile a wave at a time
 // -----------------------------------
@@ -54,7 +56,7 @@ constexpr int kWaves = 16;
 // (three or four slots measured 1.3-2.4 us slower at configuration 4).
 constexpr int kRing = 2;
 constexpr int kJobs = 3;              // loads per wave per tile (K codes, V codes, both scales)
-constexpr int kMaxChunkTiles = 128;   // the page-id table holds 2 * 128 entries
+constexpr int kMaxChunkTiles = 128;   // a wave's 2 * 128 / 16 page ids fill 16 lanes
 constexpr int kMaxChunks = 64;
 constexpr int kMergeBatch = 8;
 constexpr int kSC1 = 16;  // cache-policy bit sc1: device-coherent access
@@ -66,14 +68,14 @@ constexpr uint32_t SPAGE = 16 * 4;   // scale bytes of a page (per tensor)
 // A wave's slot (one tile): [K codes 1 KiB][V codes 1 KiB][K scales 128 B]
 // [V scales 128 B]; wave w's ring is slots w * kRing .. w * kRing + kRing - 1.
 constexpr int K_OFF = 0, V_OFF = 1024, KS_OFF = 2048, VS_OFF = 2048 + 128, SLOT = 2304;
-constexpr int PID_OFF = kWaves * kRing * SLOT;  // page-id table: 2 * kMaxChunkTiles int32
-constexpr int LDS_BYTES = PID_OFF + 4 * 2 * kMaxChunkTiles;
+constexpr int LDS_BYTES = kWaves * kRing * SLOT;
+static_assert(2 * kMaxChunkTiles / kWaves <= 64, "a wave's page ids fit its lanes");
 // Epilogue (over the ring once the loop is done): per wave [m 16][l 16]
 // [o 16 heads x 65 (64 dims, padded)] fp32.
 constexpr int EPI_ROW = 65;
 constexpr int EPI_FLOATS = 32 + 16 * EPI_ROW;
 constexpr int CTL_OFF = kWaves * EPI_FLOATS * 4;
-static_assert(CTL_OFF + 16 <= PID_OFF, "epilogue inside the ring");
+static_assert(CTL_OFF + 16 <= LDS_BYTES, "epilogue inside the ring");
 static_assert(LDS_BYTES <= 160 * 1024, "LDS of a CU");
 
 typedef int int2v_t __attribute__((ext_vector_type(2)));
@@ -164,16 +166,10 @@ __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// LDS reads of data that direct-to-LDS loads wrote (and of the page-id
-// table) are inline assembly that waits for its own results: the compiler
-// cannot tell them from the loads still streaming into the other slots and
-// would wait for those too.  A vmcnt wait and a workgroup barrier precede
-// every read of a slot.
-__device__ __forceinline__ int lds_i32(uint32_t addr) {
-    int v;
-    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
-    return v;
-}
+// LDS reads of data that direct-to-LDS loads wrote are inline assembly that
+// waits for its own results: the compiler cannot tell them from the loads
+// still streaming into the other slots and would wait for those too.  The
+// wave's own vmcnt wait precedes every read of a slot.
 // All of a tile's reads at once: K (four dwords, (half e, group g) 256
 // bytes apart), K and V scales (16 bytes of page e, 64 bytes apart) and the
 // transposed V reads of both groups.
@@ -228,9 +224,12 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
 
     // ---- the chunk's page ids (thread j: page p0 + j, clamped into the
     // table row) and q are in flight together with the sequence length.
-    const int n_pid = 2 * p_chunk_tiles;
-    int raw_pid = 0;
-    if ((int)threadIdx.x < n_pid) raw_pid = virtual_page(bt, min(p0 + (int)threadIdx.x, p_max_pages - 1), p_page_shift);
+    // Lane L < 16 of wave w: the page id of chunk page 2 (16 (L >> 1) + w) +
+    // (L & 1), clamped into the table row (this wave's tiles' pages).
+    int my_pid = 0;
+    if (lane < 2 * (kMaxChunkTiles / kWaves))
+        my_pid = virtual_page(bt, min(p0 + 2 * (kWaves * (lane >> 1) + wave) + (lane & 1), p_max_pages - 1),
+                              p_page_shift);
     // q as the QK B operand: lane (head n, k-chunk jq) holds dims
     // 32 g + 8 jq .. + 7 of head n (zero for n >= the query heads).
     const bool col_valid = n < p_n_q_heads;
@@ -254,10 +253,6 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
     // Table entries past jlim (pages past the sequence or the chunk) are
     // never read: a lookup is clamped to the last page that holds tokens.
     const int jlim = min(last_lp - p0, 2 * n_ct - 1);
-    int32_t* const ptab = reinterpret_cast<int32_t*>(smem + PID_OFF);
-    if ((int)threadIdx.x < n_pid) ptab[threadIdx.x] = raw_pid;
-    __syncthreads();
-    const uint32_t tab = lds_addr(ptab);
 
     // ---- this wave's loads of its tile number s (chunk-relative tile
     // 16 s + wave) into its ring slot s % kRing.  Per-lane parts:
@@ -279,8 +274,9 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
     auto issue = [&](int s) __attribute__((always_inline)) {
         uint8_t* const dst = ring + (s % kRing) * SLOT;
         const int t = kWaves * s + wave;  // chunk-relative tile
-        const int pa = __builtin_amdgcn_readfirstlane(lds_i32(tab + 4 * min(2 * t, jlim)));
-        const int pb = __builtin_amdgcn_readfirstlane(lds_i32(tab + 4 * min(2 * t + 1, jlim)));
+        // the tile's first page is within jlim; a second page past it is the first again
+        const int pa = __builtin_amdgcn_readlane(my_pid, 2 * s);
+        const int pb = 2 * t + 1 > jlim ? pa : __builtin_amdgcn_readlane(my_pid, 2 * s + 1);
         const uint64_t pg = (uint64_t)(uint32_t)((lane >> 5) ? pb : pa);  // K and V: lanes 32-63 read page e = 1
         const uint64_t ps = (uint64_t)(uint32_t)(((lane >> 4) & 1) ? pb : pa);
         __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.k_data + pg * KPAGE + k_lane),
