@@ -75,22 +75,24 @@ def decode_kernel_name(plan, group: int, n_kv: int, d: int, batch: int, max_page
     """Name of the decode kernel a plan runs, as rocprofv3 reports it.  16-wave
     plans: the streaming kernel for its shape (D=128, Hkv=8, 4 query heads per
     kv head) in chunk mode with at most 64 chunks, the MQA streaming kernel for
-    one kv head at D=64, else the page-streaming kernel; other plans: the general kernel (its VALU-tile variant with
-    IRIS_DECODE_KERNEL=valu)."""
-    if (plan[2] == 16 and plan[0] > 0 and plan[1] <= 64 and d == 128 and n_kv == 8 and group == 4
-            and os.environ.get("IRIS_DECODE_KERNEL") != "pages"):
+    one kv head at D=64, else the page-streaming kernel (always, with the
+    page-kernel bit in the plan's wave count); other plans: the general kernel
+    (its VALU-tile variant with the VALU bit)."""
+    waves, page_bit, valu_bit = plan[2] & 0xFF, plan[2] & 0x100, plan[2] & 0x200
+    if (waves == 16 and not page_bit and plan[0] > 0 and plan[1] <= 64 and d == 128 and n_kv == 8
+            and group == 4):
         # (rocprofv3 prints this kernel mangled: _Float16 in its signature)
         return "_ZN4iris2st25int4_decode_stream_kernelILi8ELb0EEEvPKiS3_PKDF16_iiiiiiiNS0_4ArgsE"
-    if plan[2] == 16 and n_kv == 1 and d == 64 and group <= 16 and os.environ.get("IRIS_DECODE_KERNEL") != "pages":
+    if waves == 16 and not page_bit and n_kv == 1 and d == 64 and group <= 16:
         return "_ZN4iris2mq22int4_decode_mqa_kernelEPKiS2_PKDF16_iiiiiiNS0_4ArgsE"  # (printed mangled)
-    if plan[2] == 16:
+    if waves == 16:
         gs = 4
         while gs > 1 and gs * group > 16:
             gs //= 2
         gs = min(gs, d // 32)
         return f"void iris::pg::int4_decode_pages_kernel<{d}, {gs}, {n_kv}>(iris::pg::Args)"
     kvw = kernel_kvw(group, n_kv, batch, max_pages)
-    if os.environ.get("IRIS_DECODE_KERNEL") == "valu":  # the VALU tile, measured against the MFMA one
+    if valu_bit:  # the VALU tile, measured against the MFMA one
         return f"void iris::int4_decode_valu_kernel<{d}, {kvw}>(iris::DecodeArgs)"
     return f"void iris::int4_decode_kernel<{d}, {kvw}>(iris::DecodeArgs)"
 
@@ -117,6 +119,9 @@ def parse():
     ap.add_argument("--replicas", type=int, default=0, help="cache copies to rotate (0 = auto)")
     ap.add_argument("--tokens-per-split", type=int, default=0)
     ap.add_argument("--waves-per-block", type=int, default=0)
+    ap.add_argument("--decode-kernel", choices=["auto", "pages", "valu"], default="auto",
+                    help="A/B runs: keep the page-streaming kernel for 16-wave plans (pages), or run the "
+                         "general kernel's VALU tile (valu)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample", type=int, default=0,
                     help="sequences in the CPU-baseline sample (0 = auto)")
@@ -196,8 +201,11 @@ def main() -> int:
     caches = [cache0] + [tuple(t.clone() for t in cache0) for _ in range(reps - 1)]
     q, bt, sl = (t.to(dev) for t in (case.query, case.block_table, case.seq_lens))
     out = torch.empty(q.shape, dtype=torch.float16, device=dev)
+    from iris_kernel.fused_attention import DECODE_PAGE_KERNEL, DECODE_VALU_TILE
+
+    select = {"auto": 0, "pages": DECODE_PAGE_KERNEL, "valu": DECODE_VALU_TILE}[args.decode_kernel]
     plan = decode_plan(B, Hq, Hkv, D, bt.shape[1], sum(lens), max(lens), args.tokens_per_split,
-                       args.waves_per_block)
+                       args.waves_per_block | select)
     ws = torch.zeros(max(plan[3], 1), dtype=torch.uint8, device=dev)  # counters start at zero
     torch.cuda.synchronize()
     log(f"config {args.config}: B={B} Hq={Hq} Hkv={Hkv} D={D} max L={max(lens)}; {reps} cache replicas of "

@@ -120,10 +120,23 @@ int iris_quantize_pack_int4(const void *x, void *packed, void *scales, int64_t n
  * size in bytes (0 when no sequence can need more than one chunk).
  * total_tokens and max_tokens (sum and max of seq_lens) may be -1 if
  * unknown; max_pages (columns of block_table) bounds them.
- * tokens_per_split > 0 and waves_per_block > 0 override the heuristic.
+ * tokens_per_split > 0 and waves_per_block > 0 override the heuristic:
+ * its low 8 bits ask for a wave count (16: a page-streaming kernel; 1-4:
+ * the general kernel), and one of the selection bits below may be or-ed
+ * in.  out_waves carries the wave count and the selection bit into the
+ * launch, so a plan and its launch always run the same kernel.
  * max_pages counts 16-token pages: block_table columns * page_size / 16.
  * head_dim 64, 128 or 256; any num_q_heads / num_kv_heads.
  */
+/* Kernel selection bits of waves_per_block (no reference counterpart; for
+ * A/B measurements and tests).  IRIS_DECODE_PAGE_KERNEL: 16-wave plans run
+ * the general page-streaming kernel even at the shapes the streaming
+ * (head_dim 128, 8 kv heads, 4 query heads each) or MQA (one kv head,
+ * head_dim 64) kernels cover.  IRIS_DECODE_VALU_TILE: the general kernel
+ * with VALU dot products in place of MFMA (4 query heads per kv head at
+ * head_dim 128, 16 at head_dim 64; other shapes are refused). */
+#define IRIS_DECODE_PAGE_KERNEL 0x100
+#define IRIS_DECODE_VALU_TILE 0x200
 int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                      int64_t max_pages, int64_t total_tokens, int64_t max_tokens,
                      int32_t tokens_per_split, int32_t waves_per_block, int32_t *out_chunk_tiles,

@@ -65,6 +65,26 @@ __device__ __forceinline__ float row16_sum(float x) {
     return x + dpp_f(x, 3);
 }
 
+// Non-finite values inside a sequence's valid range.  The eager attention
+// dequantises code * scale in fp32: a NaN K scale, or an infinite one (times
+// a zero code, or summed over products of both signs), makes the logits of
+// every query head of its kv head NaN, and the softmax makes those heads'
+// outputs NaN.  In the kernels a NaN score already spreads to the head's
+// softmax sum and output (p = exp2(NaN - m)); an infinite K scale (or query
+// element) instead gives a score of +-inf, since the code offset is removed
+// by a second sum whose residual need not be zero.  +inf spreads as NaN too
+// (m = inf, p = exp2(inf - inf)), but -inf would only drop its token.  With
+// finite scales and queries every score is finite, so each kernel keeps the
+// lowest score of the valid tokens it has seen and, when that is -inf,
+// poisons the head's softmax sum with kNonFinite before its outputs are
+// formed.  (The one case that differs from the eager result: an infinite
+// scale over nonzero codes whose products all have one sign, where eager
+// gives a finite result for a -inf logit and the kernels NaN.)
+constexpr float kNonFinite = __builtin_nanf("");
+__device__ __forceinline__ float poison_if_neg_inf(float lowest, float l) {
+    return lowest == -INFINITY ? kNonFinite : l;
+}
+
 // Split-KV arrival counters.  Every decode kernel keeps them in one region
 // at the head of its workspace, kCountersPerSeq uint32 per sequence
 // (sequence b's at [b * kCountersPerSeq, (b + 1) * kCountersPerSeq)), so

@@ -182,8 +182,8 @@ __device__ __forceinline__ void transpose_rows4(u32x4_t& x) {
 
 // ---- VALU tile: v_dot2c_f32_f16 with DPP row broadcasts (no MFMA)
 //
-// The alternative to the MFMA tile, selected at run time (IRIS_DECODE_KERNEL
-// = valu) for the layouts KVW * g = 16 with g = 4 or 16.  Every dot product
+// The alternative to the MFMA tile, selected per launch (the
+// IRIS_DECODE_VALU_TILE bit of waves_per_block) for the layouts KVW * g = 16 with g = 4 or 16.  Every dot product
 // is a chain of v_dot2c_f32_f16 whose first operand is broadcast from one
 // lane of the 16-lane row (DPP row_newbcast), so each fp16 pair is unpacked
 // or computed once and no operand is replicated in registers:
@@ -701,6 +701,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
 
     float m_run = -INFINITY;  // MFMA units
     float l_part = 0.0f;
+    float s_lo = INFINITY;  // lowest valid score seen
     float ps[G];
     float4_t o[G][2];
 #pragma unroll
@@ -721,7 +722,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
     //   col(rho, w) = 4 rho + w (KVW = 4: the row is a kv head) or 4 w + rho
     //   (KVW = 1), w = 0..3; softmax and PV keep that layout.
     uint32_t qv[4][G], qc[G];
-    float vm[4], vl[4], vps[G][4], vo[G][4][2];
+    float vm[4], vl[4], vlo[4], vps[G][4], vo[G][4][2];
     if constexpr (VALU) {
         const half_t s16 = (half_t)0.0625f;
 #pragma unroll
@@ -747,6 +748,7 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
         for (int w = 0; w < 4; ++w) {
             vm[w] = -INFINITY;
             vl[w] = 0.0f;
+            vlo[w] = INFINITY;
 #pragma unroll
             for (int grp = 0; grp < G; ++grp) {
                 vps[grp][w] = 0.0f;
@@ -809,13 +811,21 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
         // canonicalised operands after the masking selects; the scores are
         // finite or -inf.)
         const int nval = seq_len - tok_base - 4 * jq;
-        if (!full) {
+        float lo;  // lowest score of the valid tokens (-inf: a non-finite K scale or query)
+        if (full) {
+            lo = fminf(fminf(fminf(s[0][0], s[0][1]), fminf(s[0][2], s[0][3])),
+                       fminf(fminf(s[1][0], s[1][1]), fminf(s[1][2], s[1][3])));
+        } else {
+            lo = INFINITY;
 #pragma unroll
             for (int r = 0; r < 2; ++r)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 4; ++i) {
                     if (16 * r + i >= nval) s[r][i] = -INFINITY;
+                    else lo = fminf(lo, s[r][i]);
+                }
         }
+        s_lo = fminf(s_lo, lo);
         auto vmax = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
         float mx = vmax(vmax(vmax(s[0][0], s[0][1]), vmax(s[0][2], s[0][3])),
                         vmax(vmax(s[1][0], s[1][1]), vmax(s[1][2], s[1][3])));
@@ -992,6 +1002,14 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
             }
         }
         if (next < t_end) issue_k(next, kw);
+        {
+            // lowest score of the valid tokens per column (-inf: a non-finite
+            // K scale or query)
+            const bool v0 = full || tok_base + n < seq_len, v1 = full || tok_base + 16 + n < seq_len;
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                vlo[w] = fminf(vlo[w], fminf(v0 ? sc[0][w] : INFINITY, v1 ? sc[1][w] : INFINITY));
+        }
         if (!full) {
 #pragma unroll
             for (int r = 0; r < 2; ++r)
@@ -1106,13 +1124,13 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             vm[w] *= c24;
-            vl[w] = row16_sum(vl[w]);
+            vl[w] = row16_sum(poison_if_neg_inf(vlo[w], vl[w]));
 #pragma unroll
             for (int grp = 0; grp < G; ++grp) vps[grp][w] = 8.0f * row16_sum(vps[grp][w]);
         }
     } else {
         m_run *= c24;
-        l_part = row_sum4(l_part);
+        l_part = row_sum4(poison_if_neg_inf(s_lo, l_part));
 #pragma unroll
         for (int grp = 0; grp < G; ++grp) ps[grp] = 8.0f * row_sum4(ps[grp]);
     }
@@ -1275,7 +1293,7 @@ template <int D, int KVW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 256 ? 1 : 2))) void int4_decode_kernel(DecodeArgs a) {
     decode_body<D, KVW, false>(a);
 }
-// The VALU tile (IRIS_DECODE_KERNEL=valu; measured against the MFMA tile).
+// The VALU tile (IRIS_DECODE_VALU_TILE; measured against the MFMA tile).
 template <int D, int KVW>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void int4_decode_valu_kernel(DecodeArgs a) {
     decode_body<D, KVW, true>(a);
@@ -1338,23 +1356,32 @@ constexpr int64_t kPagesMinBytes = 100000000;  // K/V bytes above which the page
 // pages_waves() (16) waves per workgroup, the general kernel here with 1-4,
 // so the plan's waves_per_block names the kernel for the launch.  A plan
 // asked for 16 waves uses the page kernel wherever it supports the shape;
-// asked for 1-4, or with IRIS_DECODE_KERNEL=general in the environment (A/B
-// measurements), the general kernel; IRIS_DECODE_KERNEL=valu runs the general
-// kernel with its VALU tile instead of MFMA (g = 4 at D = 128, g = 16 at
-// D = 64; other shapes are refused).  Left to choose, the plan takes the page
-// kernel where it is the faster one: head_dim 128 with at most 4 query heads
-// per kv head and at least 4 kv heads (8 KB page slabs, the GQA shapes of
-// 7-70B models), over batches of similar lengths (its one workgroup per CU
-// balances ragged batches worse than the general kernel's many small ones)
-// that read at least kPagesMinBytes of K/V.
-static bool valu_selected() {
-    const char* sel = getenv("IRIS_DECODE_KERNEL");
-    return sel != nullptr && strcmp(sel, "valu") == 0;
+// asked for 1-4, the general kernel.  Two selection bits above the wave
+// count (IRIS_DECODE_PAGE_KERNEL, IRIS_DECODE_VALU_TILE of iris_hip.h), for
+// A/B measurements and tests, travel from the plan's waves_per_block into
+// its out_waves and so into the launch: the first keeps the page kernel
+// itself for 16-wave plans (no streaming or MQA kernel), the second runs
+// the general kernel with its VALU tile instead of MFMA (g = 4 at D = 128,
+// g = 16 at D = 64; other shapes are refused).  Left to choose, the plan
+// takes the page kernel where it is the faster one: head_dim 128 with at
+// most 4 query heads per kv head and at least 4 kv heads (8 KB page slabs,
+// the GQA shapes of 7-70B models), over batches of similar lengths (its one
+// workgroup per CU balances ragged batches worse than the general kernel's
+// many small ones) that read at least kPagesMinBytes of K/V.
+constexpr int32_t kWaveMask = 0xFF;
+constexpr int32_t kPageKernel = IRIS_DECODE_PAGE_KERNEL;
+constexpr int32_t kValuTile = IRIS_DECODE_VALU_TILE;
+// The selection bits of waves_per_block, or -1 if it is not a valid request.
+static int32_t selection_of(int32_t waves_per_block) {
+    if (waves_per_block < 0) return 0;  // (as 0: let the plan choose)
+    const int32_t sel = waves_per_block & ~kWaveMask;
+    if ((sel & ~(kPageKernel | kValuTile)) != 0 || sel == (kPageKernel | kValuTile)) return -1;
+    return sel;
 }
+static int32_t waves_of(int32_t waves_per_block) { return waves_per_block < 0 ? 0 : waves_per_block & kWaveMask; }
 static bool pages_allowed(int32_t waves_per_block) {
-    const char* sel = getenv("IRIS_DECODE_KERNEL");
-    if (sel != nullptr && (strcmp(sel, "general") == 0 || strcmp(sel, "valu") == 0)) return false;
-    return waves_per_block <= 0 || waves_per_block == pages_waves();
+    const int32_t w = waves_of(waves_per_block);
+    return (selection_of(waves_per_block) & kValuTile) == 0 && (w == 0 || w == pages_waves());
 }
 static bool pages_preferred(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                             int64_t total_tokens, int64_t max_tokens, bool lengths_known) {
@@ -1375,13 +1402,11 @@ static bool pages_preferred(int64_t batch, int64_t num_q_heads, int64_t num_kv_h
 // plan takes it for batches of similar lengths with at least kMqaMinBytes of
 // K/V to read (configuration 4: B=128, L=8192, 76 MB); smaller or ragged
 // batches go to the general kernel's many small chunks.
-// IRIS_DECODE_KERNEL=pages forces the page kernel for A/B runs.
+// IRIS_DECODE_PAGE_KERNEL keeps the page kernel instead, for A/B runs.
 constexpr int64_t kMqaMinBytes = 16000000;
 static bool mqa_allowed(int32_t waves_per_block) {
-    const char* sel = getenv("IRIS_DECODE_KERNEL");
-    if (sel != nullptr && (strcmp(sel, "general") == 0 || strcmp(sel, "valu") == 0 || strcmp(sel, "pages") == 0))
-        return false;
-    return waves_per_block <= 0 || waves_per_block == mqa_waves();
+    const int32_t w = waves_of(waves_per_block);
+    return selection_of(waves_per_block) == 0 && (w == 0 || w == mqa_waves());
 }
 static bool mqa_preferred(int64_t batch, int64_t total_tokens, int64_t max_tokens) {
     if (total_tokens * (64 + 8) < kMqaMinBytes) return false;
@@ -1399,21 +1424,26 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
     if (batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
         (head_dim != 64 && head_dim != 128 && head_dim != 256) || max_pages <= 0 || max_pages > 0x3FFFFFFF)
         return kInvalidArgument;
+    const int32_t sel = selection_of(waves_per_block);
+    if (sel < 0) return kInvalidArgument;
     // Unknown lengths (the sync-free positional handle): the widest batch
     // block_table admits stands in for them.
     const int64_t est_max = max_tokens < 0 ? max_pages * kPageSize : max_tokens;
     const int64_t est_total = total_tokens < 0 ? batch * est_max : total_tokens;
     if (mqa_allowed(waves_per_block) && mqa_supported(num_q_heads, num_kv_heads, head_dim) &&
-        (waves_per_block == mqa_waves() || mqa_preferred(batch, est_total, est_max)) &&
+        (waves_of(waves_per_block) == mqa_waves() || mqa_preferred(batch, est_total, est_max)) &&
         mqa_plan(batch, num_q_heads, head_dim, max_pages, max_tokens, tokens_per_split, out_chunk_tiles,
                  out_max_chunks, out_waves, out_workspace_bytes) == kOk)
         return kOk;
     if (pages_allowed(waves_per_block) && pages_supported(num_q_heads, num_kv_heads, head_dim, max_pages) &&
-        (waves_per_block == pages_waves() ||
+        (waves_of(waves_per_block) == pages_waves() ||
          pages_preferred(batch, num_q_heads, num_kv_heads, head_dim, est_total, est_max,
-                         total_tokens >= 0 && max_tokens >= 0)))
-        return pages_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, total_tokens, max_tokens,
-                          tokens_per_split, out_chunk_tiles, out_max_chunks, out_waves, out_workspace_bytes);
+                         total_tokens >= 0 && max_tokens >= 0))) {
+        const int st = pages_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, total_tokens, max_tokens,
+                                  tokens_per_split, out_chunk_tiles, out_max_chunks, out_waves, out_workspace_bytes);
+        if (st == kOk) *out_waves |= sel & kPageKernel;
+        return st;
+    }
     const int g = (int)(num_q_heads / num_kv_heads);
     const int kvw = pick_kvw(g, (int)num_kv_heads, batch, max_pages, head_dim);
     const int64_t n_kvb = num_kv_heads / kvw * query_blocks(g);
@@ -1424,7 +1454,7 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
     // cannot see a length it was not planned for); the measured lengths only
     // steer the chunk size.
     const int64_t max_tiles = (cap_tokens + kTile - 1) / kTile;
-    int nw = waves_per_block > 0 ? waves_per_block : 4;
+    int nw = waves_of(waves_per_block) > 0 ? waves_of(waves_per_block) : 4;
     if (nw > 4) nw = 4;
     int64_t chunk_tiles;
     if (tokens_per_split > 0) {
@@ -1464,7 +1494,7 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
     if (max_chunks > 1 && n_kvb > kCountersPerSeq) return kInvalidArgument;
     *out_chunk_tiles = (int32_t)chunk_tiles;
     *out_max_chunks = (int32_t)max_chunks;
-    *out_waves = nw;
+    *out_waves = nw | (sel & kValuTile);
     *out_workspace_bytes = max_chunks > 1 ? workspace_bytes(batch, n_kvb, max_chunks, head_dim) : 0;
     return kOk;
 }
@@ -1487,18 +1517,22 @@ extern "C" int iris_int4_paged_decode_attention(
         return kInvalidArgument;
     const int64_t bt_cols = max_pages;
     max_pages <<= shift;
-    if (waves_per_block == mqa_waves() && mqa_allowed(waves_per_block) &&
+    const int32_t sel = selection_of(waves_per_block);
+    if (sel < 0) return kInvalidArgument;
+    const int32_t waves = waves_of(waves_per_block);
+    if (waves == mqa_waves() && mqa_allowed(waves_per_block) &&
         mqa_supported(num_q_heads, num_kv_heads, head_dim) && chunk_tiles > 0)
         return mqa_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
                           workspace, workspace_bytes_avail, batch, num_q_heads, max_pages, bt_cols, shift,
                           softmax_scale, chunk_tiles, max_chunks, stream);
-    if (waves_per_block == pages_waves() && pages_allowed(waves_per_block) &&
+    if (waves == pages_waves() && pages_allowed(waves_per_block) &&
         pages_supported(num_q_heads, num_kv_heads, head_dim, max_pages))
         return pages_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
                             workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, max_pages,
-                            bt_cols, shift, softmax_scale, chunk_tiles, max_chunks, stream);
-    if (chunk_tiles <= 0 || chunk_tiles > kMaxChunkTiles || max_chunks <= 0 || waves_per_block <= 0 ||
-        waves_per_block > 4)
+                            bt_cols, shift, softmax_scale, chunk_tiles, max_chunks, (sel & kPageKernel) == 0,
+                            stream);
+    if (chunk_tiles <= 0 || chunk_tiles > kMaxChunkTiles || max_chunks <= 0 || waves <= 0 || waves > 4 ||
+        (sel & kPageKernel) != 0)
         return kInvalidArgument;
     if ((int64_t)chunk_tiles * max_chunks * 2 < max_pages) return kInvalidArgument;
     const int g = (int)(num_q_heads / num_kv_heads);
@@ -1540,24 +1574,24 @@ extern "C" int iris_int4_paged_decode_attention(
     const int64_t nblocks = batch * a.n_kv_blocks * (int64_t)max_chunks;
     if (nblocks > 0x7FFFFFFF) return kInvalidArgument;
     hipStream_t s = (hipStream_t)stream;
-    const dim3 grid((unsigned)nblocks), block(64 * waves_per_block);
+    const dim3 grid((unsigned)nblocks), block(64 * waves);
     int st;
-    if (valu_selected()) {
+    if ((sel & kValuTile) != 0) {
         // The VALU tile covers the two layouts with 16 columns of one or four
         // kv heads: g = 4 at D = 128 (KVW 4) and g = 16 at D = 64 (KVW 1).
-        if (head_dim == 128 && kvw == 4 && g == 4) st = launch_decode<128, 4, true>(grid, block, waves_per_block, s, a);
-        else if (head_dim == 64 && kvw == 1 && g == 16) st = launch_decode<64, 1, true>(grid, block, waves_per_block, s, a);
+        if (head_dim == 128 && kvw == 4 && g == 4) st = launch_decode<128, 4, true>(grid, block, waves, s, a);
+        else if (head_dim == 64 && kvw == 1 && g == 16) st = launch_decode<64, 1, true>(grid, block, waves, s, a);
         else return kInvalidArgument;
     } else if (head_dim == 128) {
-        if (kvw == 4) st = launch_decode<128, 4>(grid, block, waves_per_block, s, a);
-        else if (kvw == 2) st = launch_decode<128, 2>(grid, block, waves_per_block, s, a);
-        else st = launch_decode<128, 1>(grid, block, waves_per_block, s, a);
+        if (kvw == 4) st = launch_decode<128, 4>(grid, block, waves, s, a);
+        else if (kvw == 2) st = launch_decode<128, 2>(grid, block, waves, s, a);
+        else st = launch_decode<128, 1>(grid, block, waves, s, a);
     } else if (head_dim == 256) {
-        st = launch_decode<256, 1>(grid, block, waves_per_block, s, a);
+        st = launch_decode<256, 1>(grid, block, waves, s, a);
     } else {
-        if (kvw == 4) st = launch_decode<64, 4>(grid, block, waves_per_block, s, a);
-        else if (kvw == 2) st = launch_decode<64, 2>(grid, block, waves_per_block, s, a);
-        else st = launch_decode<64, 1>(grid, block, waves_per_block, s, a);
+        if (kvw == 4) st = launch_decode<64, 4>(grid, block, waves, s, a);
+        else if (kvw == 2) st = launch_decode<64, 2>(grid, block, waves, s, a);
+        else st = launch_decode<64, 1>(grid, block, waves, s, a);
     }
     if (st != kOk || hipGetLastError() != hipSuccess) return kLaunchError;
     return kOk;

@@ -327,6 +327,7 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
     const float lazy = 2.0f / c24;                 // rescale when a maximum grows by more (base 2)
     float m_run = -INFINITY;                       // MFMA units
     float l_part = 0.0f;
+    float s_lo = INFINITY;                         // lowest valid score seen
     // oc8[g]: 8 * 2^-24 * (sum of the PV weights of group g) in every row,
     // the V code offset, accumulated by an MFMA with a constant A operand.
     float4_t oc8[G];
@@ -362,13 +363,21 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
             }
         }
         const int nval = seq_len - tok0 - 4 * jq;
-        if (!full) {
+        float lo;  // lowest score of the valid tokens (-inf: a non-finite K scale or query)
+        if (full) {
+            lo = fminf(fminf(fminf(s[0][0], s[0][1]), fminf(s[0][2], s[0][3])),
+                       fminf(fminf(s[1][0], s[1][1]), fminf(s[1][2], s[1][3])));
+        } else {
+            lo = INFINITY;
 #pragma unroll
             for (int e = 0; e < 2; ++e)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 4; ++i) {
                     if (16 * e + i >= nval) s[e][i] = -INFINITY;
+                    else lo = fminf(lo, s[e][i]);
+                }
         }
+        s_lo = fminf(s_lo, lo);
         auto vmax = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
         float mx = vmax(vmax(vmax(s[0][0], s[0][1]), vmax(s[0][2], s[0][3])),
                         vmax(vmax(s[1][0], s[1][1]), vmax(s[1][2], s[1][3])));
@@ -451,7 +460,7 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
     // ---- each wave's (m, l, o) in LDS area `wave`: [0, 16) m (base-2
     // logits), [16, 32) l, [32 + h EPI_ROW + d] o (code offset removed).
     {
-        l_part = row_sum4(l_part);
+        l_part = row_sum4(poison_if_neg_inf(s_lo, l_part));
         float psr[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) psr[g] = oc8[g][0] * 16777216.0f;

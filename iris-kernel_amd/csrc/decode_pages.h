@@ -30,6 +30,6 @@ IRIS_INTERNAL int pages_launch(const void* query, const void* k_data, const void
                                int32_t output_is_f32, void* workspace, int64_t workspace_bytes_avail, int64_t batch,
                                int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t max_pages,
                                int64_t bt_cols, int32_t page_mul, float softmax_scale, int32_t chunk_tiles,
-                               int32_t max_chunks, void* stream);
+                               int32_t max_chunks, bool allow_stream, void* stream);
 
 }  // namespace iris

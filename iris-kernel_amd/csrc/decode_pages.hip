@@ -539,6 +539,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void int4_decode_pages_kernel(Args 
     const float lazy = 2.0f / c24;
     float m_run = -INFINITY;
     float l_part = 0.0f;
+    float s_lo = INFINITY;  // lowest valid score seen
     float ps[NP];
     float4_t o[NP][2];
 #pragma unroll
@@ -583,13 +584,21 @@ __global__ __launch_bounds__(64 * kMaxWaves) void int4_decode_pages_kernel(Args 
 #pragma unroll
             for (int i = 0; i < 4; ++i) s[r][i] = group_sum<GS>(s[r][i]);
         // ---- online softmax (base 2, lazy rescale)
-        if (!full) {
+        float lo;  // lowest score of the valid tokens (-inf: a non-finite K scale or query)
+        if (full) {
+            lo = fminf(fminf(fminf(s[0][0], s[0][1]), fminf(s[0][2], s[0][3])),
+                       fminf(fminf(s[1][0], s[1][1]), fminf(s[1][2], s[1][3])));
+        } else {
+            lo = INFINITY;
 #pragma unroll
             for (int r = 0; r < 2; ++r)
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 4; ++i) {
                     if (tok0 + 16 * r + 4 * jq + i >= seq_len) s[r][i] = -INFINITY;
+                    else lo = fminf(lo, s[r][i]);
+                }
         }
+        s_lo = fminf(s_lo, lo);
         float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                          fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
         mx = row_max4(mx);  // finite: token tok0 < seq_len
@@ -690,7 +699,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void int4_decode_pages_kernel(Args 
 
     // ---- final per-lane values: undo the code offset and the 2^-24 units
     m_run *= c24;
-    l_part = row_sum4(l_part);
+    l_part = row_sum4(poison_if_neg_inf(s_lo, l_part));
 #pragma unroll
     for (int p = 0; p < NP; ++p) ps[p] = 8.0f * row_sum4(ps[p]);
 
@@ -990,11 +999,6 @@ namespace {
 
 constexpr int kWaves = 16;  // every (Hkv, head_dim) layout runs 16 waves per workgroup
 
-bool stream_allowed() {
-    const char* sel = getenv("IRIS_DECODE_KERNEL");
-    return sel == nullptr || strcmp(sel, "pages") != 0;
-}
-
 // Scale slots per query head: as many of the G groups as fit beside the
 // group's query heads in the 16 MFMA columns.
 int pick_gs(int g, int head_dim) {
@@ -1164,7 +1168,7 @@ int pages_launch(const void* query, const void* k_data, const void* v_data, cons
                  const int32_t* block_table, const int32_t* seq_lens, void* output, int32_t output_is_f32,
                  void* workspace, int64_t workspace_bytes_avail, int64_t batch, int64_t num_q_heads,
                  int64_t num_kv_heads, int64_t head_dim, int64_t max_pages, int64_t bt_cols, int32_t page_shift,
-                 float softmax_scale, int32_t chunk_tiles, int32_t max_chunks, void* stream) {
+                 float softmax_scale, int32_t chunk_tiles, int32_t max_chunks, bool allow_stream, void* stream) {
     const int hkv = (int)num_kv_heads;
     // chunk_tiles > 0: chunk mode, batch x max_chunks workgroups of
     // chunk_tiles tiles; < 0: the balanced mode, max_chunks workgroups
@@ -1173,10 +1177,10 @@ int pages_launch(const void* query, const void* k_data, const void* v_data, cons
     const int64_t share = balanced ? -(int64_t)chunk_tiles : chunk_tiles;
     if (share <= 0 || share > pg::kMaxChunkTiles || max_chunks <= 0) return kInvalidArgument;
     // The shapes the streaming kernel has (decode_stream.hip), in either
-    // mode: it runs them instead (IRIS_DECODE_KERNEL=pages keeps this kernel,
-    // for A/B measurements).  Its workspace layout is this kernel's.
-    if (stream_supported(num_q_heads, num_kv_heads, head_dim) &&
-        (balanced ? max_chunks <= 8 * pg::kMaxGroups : max_chunks <= stream_max_chunks()) && stream_allowed())
+    // mode: it runs them instead (allow_stream false keeps this kernel, for
+    // A/B measurements).  Its workspace layout is this kernel's.
+    if (allow_stream && stream_supported(num_q_heads, num_kv_heads, head_dim) &&
+        (balanced ? max_chunks <= 8 * pg::kMaxGroups : max_chunks <= stream_max_chunks()))
         return stream_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
                              workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, max_pages,
                              bt_cols, page_shift, softmax_scale, chunk_tiles, max_chunks, stream);

@@ -587,7 +587,10 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
             s = __builtin_fmaf((float)k01.y, acc[e][1], s);
             s = __builtin_fmaf((float)k23.x, acc[e][2], s);
             s = __builtin_fmaf((float)k23.y, acc[e][3], s);
-            t[e] = s * c24;
+            // base-2 logit; s - s is 0 for a finite score and NaN for +-inf,
+            // so a non-finite K scale or query gives NaN as the eager
+            // dequantisation does, never a -inf that would drop the token
+            t[e] = __builtin_fmaf(s, c24, s - s);
         }
         if (tok0 + kTile > seq_len) {
 #pragma unroll

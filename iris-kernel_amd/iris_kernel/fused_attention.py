@@ -12,7 +12,9 @@ Additions, all keyword-only and defaulted so existing calls are unchanged:
 ``tokens_per_split`` / ``waves_per_block`` override the split heuristic,
 ``workspace`` supplies the split-KV buffer (its head holds 128 arrival
 counters per sequence, which every call leaves at zero; the wrapper zeroes
-that region whenever a call's batch exceeds the previous call's).  Without one, a
+that region the first time it sees a workspace tensor and whenever a call's
+batch exceeds the previous call's with it; nothing else may write it between
+calls).  Without one, a
 zero-filled workspace is cached per (device, stream), so calls on one stream
 share it safely and calls on different streams never do.  An fp32 ``output``
 tensor receives the values before the final fp16 rounding (test aid).
@@ -25,13 +27,23 @@ baseline (fused_attention.py:528-582, kernel :223-370) over an fp16 cache
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import torch
 
 from . import _lib
 
 __all__ = ["fused_int4_paged_decode_attention", "_int4_paged_decode_attention", "decode_plan",
-           "fused_fp16_paged_decode_attention", "_fp16_paged_decode_attention", "fp16_decode_plan"]
+           "fused_fp16_paged_decode_attention", "_fp16_paged_decode_attention", "fp16_decode_plan",
+           "DECODE_PAGE_KERNEL", "DECODE_VALU_TILE"]
+
+# Kernel selection bits or-ed into ``waves_per_block`` (IRIS_DECODE_PAGE_KERNEL
+# and IRIS_DECODE_VALU_TILE of include/iris_hip.h), for A/B measurements and
+# tests: 16-wave plans keep the general page-streaming kernel, or the general
+# kernel runs its VALU tile.  The plan returns them in its wave count, so its
+# launch runs the kernel it planned.
+DECODE_PAGE_KERNEL = 0x100
+DECODE_VALU_TILE = 0x200
 
 
 def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, max_pages: int,
@@ -100,8 +112,11 @@ def counter_region_bytes(batch: int) -> int:
     return (batch * _COUNTERS_PER_SEQ * 4 + 255) // 256 * 256
 
 
-# workspace (pointer, bytes) -> the batch whose counter region is known to be zero
-_ZEROED: dict[tuple[int, int], int] = {}
+# id(workspace tensor) -> (data_ptr, bytes, batch): the batch whose counter
+# region is known to be zero in that tensor.  An entry lives exactly as long
+# as its tensor (a finalizer removes it), so a new tensor that the caching
+# allocator places where an old workspace was is never taken for zeroed.
+_ZEROED: dict[int, tuple[int, int, int]] = {}
 
 
 def _ready_workspace(device: torch.device, ws_bytes: int, batch: int,
@@ -110,20 +125,26 @@ def _ready_workspace(device: torch.device, ws_bytes: int, batch: int,
 
     Every kernel keeps its counters at the head of the workspace, 128 per
     sequence, and leaves them at zero; the bytes after them hold partial
-    results that each call rewrites.  A call with batch B therefore finds
-    the counters of sequences below the last call's batch at zero; only when
-    B exceeds that batch does the counter region need a fill (one small fill
-    kernel on the current stream)."""
+    results that each call rewrites.  The first call that sees a workspace
+    tensor zero-fills its counter region (one small fill kernel on the
+    current stream); later calls with the same tensor object find the
+    counters of sequences below the last call's batch at zero and fill only
+    when the batch grows.  Between calls the workspace's bytes belong to the
+    library: nothing else may write them."""
     if workspace is None:
         workspace = _stream_workspace(device, ws_bytes)
     elif workspace.numel() * workspace.element_size() < ws_bytes:
         raise ValueError(f"workspace must hold at least {ws_bytes} bytes")
     elif not workspace.is_contiguous():
         raise ValueError("workspace must be contiguous")
-    key = (workspace.data_ptr(), workspace.numel() * workspace.element_size())
-    if _ZEROED.get(key, 0) < batch:
+    key = id(workspace)
+    where = (workspace.data_ptr(), workspace.numel() * workspace.element_size())
+    entry = _ZEROED.get(key)
+    if entry is None or entry[:2] != where or entry[2] < batch:
         workspace.reshape(-1).view(torch.uint8)[:counter_region_bytes(batch)].zero_()
-    _ZEROED[key] = batch  # the partials of this call may overwrite counters of later sequences
+        if entry is None:
+            weakref.finalize(workspace, _ZEROED.pop, key, None)
+    _ZEROED[key] = (*where, batch)  # the partials of this call may overwrite counters of later sequences
     return workspace
 
 

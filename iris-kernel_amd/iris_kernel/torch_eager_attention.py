@@ -169,6 +169,8 @@ def torch_eager_int4_paged_decode_attention(
         page_size=page_size, group_size=group_size)
     scale = float(head_dim ** -0.5 if softmax_scale is None else softmax_scale)
     out = torch.empty_like(query)
+    if batch == 0:  # the reference's per-sequence loop runs zero times
+        return out
     # sequences in slices of bounded fp32 K/V size
     longest = int(seq_lens.max())
     per_seq = longest * k_data.shape[2] * head_dim * 8
@@ -217,6 +219,8 @@ def torch_eager_fp16_paged_decode_attention(
     if bool((used & ((ids < 0) | (ids >= num_pages))).any()):
         raise IndexError("block_table contains an invalid page id")
     scale = float(head_dim ** -0.5 if softmax_scale is None else softmax_scale)
+    if batch == 0:  # the reference's per-sequence loop runs zero times
+        return torch.empty_like(query)
     n_pages = -(-int(seq_lens.max()) // page_size)
     k = _gather_tokens(k_cache, block_table, n_pages).float()
     v = _gather_tokens(v_cache, block_table, n_pages).float()

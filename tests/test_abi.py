@@ -238,33 +238,49 @@ def test_append_check_rejects_bad_arguments_before_launch():
     assert lib.iris_append_check(p, p, -1, 64, 10, p, p, 2, None, None) == 1     # negative count
 
 
-def test_decode_kernel_environment_switch(monkeypatch):
+def test_decode_kernel_selection_bits(monkeypatch):
+    # The kernel a plan names travels in its wave count (selection bits
+    # above the low byte); nothing in the environment changes it.
+    from iris_kernel.fused_attention import DECODE_PAGE_KERNEL, DECODE_VALU_TILE
+
     shape = (32, 32, 8, 128, 256, 32 * 4096, 4096)
     assert decode_plan(*shape)[2] == 16
-    monkeypatch.setenv("IRIS_DECODE_KERNEL", "general")
-    assert decode_plan(*shape)[2] == 4
-    assert decode_plan(*shape, waves_per_block=16)[2] == 4
+    monkeypatch.setenv("IRIS_DECODE_KERNEL", "general")  # the retired switch is ignored
+    assert decode_plan(*shape)[2] == 16
+    assert decode_plan(*shape, waves_per_block=4)[2] == 4
+    assert decode_plan(*shape, waves_per_block=16 | DECODE_PAGE_KERNEL)[2] == 16 | DECODE_PAGE_KERNEL
+    assert decode_plan(*shape, waves_per_block=DECODE_VALU_TILE)[2] == 4 | DECODE_VALU_TILE
+    assert decode_plan(*shape, waves_per_block=16 | DECODE_VALU_TILE)[2] == 4 | DECODE_VALU_TILE
+    # MQA shape: a 16-wave plan runs the MQA kernel unless the page kernel is asked for
+    mqa = (128, 16, 1, 64, 512, 128 * 8192, 8192)
+    assert decode_plan(*mqa)[2] == 16
+    assert decode_plan(*mqa, waves_per_block=DECODE_PAGE_KERNEL)[2] in (16 | DECODE_PAGE_KERNEL, 4)
+    with pytest.raises(RuntimeError):
+        decode_plan(*shape, waves_per_block=DECODE_PAGE_KERNEL | DECODE_VALU_TILE)
+    with pytest.raises(RuntimeError):
+        decode_plan(*shape, waves_per_block=0x400)
 
 
-def test_valu_tile_switch_covers_two_layouts(monkeypatch):
-    # IRIS_DECODE_KERNEL=valu plans the general kernel and runs its VALU tile
-    # for g = 4 at D = 128 (four kv heads a wave) and g = 16 at D = 64; every
-    # other shape is refused before any HIP call (null pointers are safe).
-    shape = (32, 32, 8, 128, 256, 32 * 4096, 4096)
-    monkeypatch.setenv("IRIS_DECODE_KERNEL", "valu")
-    assert decode_plan(*shape)[2] == 4
-    assert decode_plan(*shape, waves_per_block=16)[2] == 4
+def test_valu_tile_selection_covers_two_layouts():
+    # The VALU bit plans the general kernel and runs its VALU tile for g = 4
+    # at D = 128 (four kv heads a wave) and g = 16 at D = 64; every other
+    # shape is refused before any HIP call (null pointers are safe).  The
+    # page-kernel bit on a general-kernel wave count is refused too.
+    from iris_kernel.fused_attention import DECODE_PAGE_KERNEL, DECODE_VALU_TILE
+
     lib = _lib.lib()
     null = None
-    def call(B, Hq, Hkv, D, maxP):
+    def call(B, Hq, Hkv, D, maxP, waves=4 | DECODE_VALU_TILE):
         return lib.iris_int4_paged_decode_attention(null, null, null, null, null, null, null, null, 0,
                                                     null, 0, B, Hq, Hkv, D, 16, 8, maxP, ctypes.c_float(0.1),
-                                                    64, (maxP + 127) // 128, 4, null)
+                                                    64, (maxP + 127) // 128, waves, null)
     assert call(2, 8, 2, 64, 4) == 1       # g = 4 at D = 64
     assert call(2, 8, 2, 128, 4) == 1      # g = 4 at D = 128, but two kv heads a wave
     assert call(2, 16, 2, 128, 4) == 1     # g = 8
     assert call(2, 16, 1, 256, 4) == 1     # D = 256
     assert call(2, 16, 4, 128, 4) == 1     # g = 4, Hkv = 4: one kv head a wave at this size
+    assert call(2, 16, 4, 128, 4, 4 | DECODE_PAGE_KERNEL) == 1
+    assert call(2, 16, 4, 128, 4, 4 | DECODE_PAGE_KERNEL | DECODE_VALU_TILE) == 1
 
 
 def test_fused_api_requires_a_gpu_when_none_is_present():

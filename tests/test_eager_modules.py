@@ -232,3 +232,19 @@ def test_decode_errors_match():
         with pytest.raises(type(want.value)) as got:
             pkg_attn.torch_eager_int4_paged_decode_attention(qq, *c, b, s)
         assert str(got.value) == str(want.value)
+
+
+def test_empty_batch_matches_reference_loop():
+    """B = 0: the reference's per-sequence loops run zero times and return an
+    empty [0, Hq, D] tensor (torch_eager_attention.py:188-239, :270-294);
+    the package's batched forms return the same instead of reducing over an
+    empty length tensor."""
+    q, cache, bt, sl = _decode_case(9, 2, 8, 2, 64, [20, 40], 8)
+    q0, bt0, sl0 = q[:0], bt[:0], sl[:0]
+    got = pkg_attn.torch_eager_int4_paged_decode_attention(q0, *cache, bt0, sl0)
+    want = ora_attn.torch_eager_int4_paged_decode_attention(q0, *cache, bt0, sl0)
+    assert got.shape == want.shape == (0, 8, 64) and got.dtype == want.dtype == torch.float16
+    kc = torch.zeros(4, 16, 2, 64, dtype=torch.float16)
+    got16 = pkg_attn.torch_eager_fp16_paged_decode_attention(q0, kc, kc, bt0, sl0)
+    want16 = ora_attn.torch_eager_fp16_paged_decode_attention(q0, kc, kc, bt0, sl0)
+    assert got16.shape == want16.shape == (0, 8, 64) and got16.dtype == torch.float16

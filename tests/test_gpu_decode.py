@@ -15,7 +15,8 @@ import torch
 
 from helpers import assert_attention_close, eager_fp32, fill_cpu, fill_gpu, log, to
 from iris_kernel import workloads
-from iris_kernel.fused_attention import _int4_paged_decode_attention, decode_plan, fused_int4_paged_decode_attention
+from iris_kernel.fused_attention import (DECODE_PAGE_KERNEL, DECODE_VALU_TILE, _int4_paged_decode_attention,
+                                         decode_plan, fused_int4_paged_decode_attention)
 from oracle import c_oracle
 from oracle.torch_eager_attention import torch_eager_int4_paged_decode_attention
 
@@ -70,16 +71,15 @@ def test_config_decode_matches_eager(device, cfg, kernel):
 
 
 @pytest.mark.parametrize("cfg", [2, 3])
-def test_page_kernel_forced_matches_eager(device, cfg, monkeypatch):
+def test_page_kernel_forced_matches_eager(device, cfg):
     # At the streaming kernel's shape a 16-wave plan runs the streaming
-    # kernel (chunk mode at cfg2, balanced mode at cfg3);
-    # IRIS_DECODE_KERNEL=pages keeps the page-streaming kernel, which must
+    # kernel (chunk mode at cfg2, balanced mode at cfg3); the
+    # DECODE_PAGE_KERNEL bit keeps the page-streaming kernel, which must
     # hold the same contract.
-    monkeypatch.setenv("IRIS_DECODE_KERNEL", "pages")
     case, cpu, gpu = prepared(cfg, device)
     if cfg not in _WANT:
         _WANT[cfg] = eager_fp32(case, cpu)
-    got = run(case, gpu, device, torch.float32, waves_per_block=16)
+    got = run(case, gpu, device, torch.float32, waves_per_block=16 | DECODE_PAGE_KERNEL)
     e = assert_attention_close(got, _WANT[cfg], f"cfg{cfg} page kernel forced")
     log(f"decode: config {cfg} page kernel forced max-abs err {e:.2e}")
 
@@ -205,25 +205,24 @@ def test_balanced_split_ragged_batches(device, case):
 
 
 @pytest.mark.parametrize("kernel", ["stream", "pages"])
-def test_stale_balanced_plan_writes_nan(device, kernel, monkeypatch):
+def test_stale_balanced_plan_writes_nan(device, kernel):
     # A balanced plan made for short ragged lengths, launched (through the
     # C ABI's launch path) with lengths whose tiles exceed what its ranges
     # can cover: every output element is NaN, not a silently truncated
     # result, and the workspace stays usable for the next correct call.  At
     # this shape the streaming kernel's balanced mode runs the plan, or the
-    # page-streaming kernel with IRIS_DECODE_KERNEL=pages.
+    # page-streaming kernel with the DECODE_PAGE_KERNEL bit.
     from iris_kernel import fused_attention as fa
 
-    if kernel == "pages":
-        monkeypatch.setenv("IRIS_DECODE_KERNEL", "pages")
+    waves = 16 | (DECODE_PAGE_KERNEL if kernel == "pages" else 0)
 
     case, cpu, gpu = prepared(2, device)
     q, bt, full = to(device, case.query, case.block_table, case.seq_lens)
     B, hq, d = q.shape
     short = torch.full((B,), 40, dtype=torch.int32)
     short[::2] = 700
-    plan = decode_plan(B, hq, 8, d, bt.shape[1], int(short.sum()), int(short.max()), 0, 16)
-    assert plan[0] < 0 and plan[2] == 16, plan
+    plan = decode_plan(B, hq, 8, d, bt.shape[1], int(short.sum()), int(short.max()), 0, waves)
+    assert plan[0] < 0 and plan[2] == waves, plan
     assert 32 * (4096 // 32) > 64 * plan[1], plan  # the full lengths outgrow it
     ws = torch.zeros(max(plan[3], 1), dtype=torch.uint8, device=device)
     out = torch.empty(B, hq, d, dtype=torch.float32, device=device)
@@ -555,32 +554,30 @@ def test_mqa_kernel_nan_tail_and_repeat(device):
 
 
 # ------------------------------------------------------------------ VALU tile
-# IRIS_DECODE_KERNEL=valu: the general kernel with v_dot2c chains (DPP row
+# DECODE_VALU_TILE: the general kernel with v_dot2c chains (DPP row
 # broadcasts) in place of its MFMAs -- the alternative the MFMA tile is
 # measured against -- held to the same contract on the layouts it covers
 # (g = 4 at D = 128 with four kv heads a wave, g = 16 at D = 64).
 @pytest.mark.parametrize("cfg", [2, 3, 4])
-def test_valu_tile_matches_eager(device, cfg, monkeypatch):
-    monkeypatch.setenv("IRIS_DECODE_KERNEL", "valu")
+def test_valu_tile_matches_eager(device, cfg):
     case, cpu, gpu = prepared(cfg, device)
     if cfg not in _WANT:
         log(f"decode: config {cfg} checker")
         _WANT[cfg] = eager_fp32(case, cpu)
     want32 = _WANT[cfg]
-    got32 = run(case, gpu, device, torch.float32, waves_per_block=4)
+    got32 = run(case, gpu, device, torch.float32, waves_per_block=4 | DECODE_VALU_TILE)
     e32 = assert_attention_close(got32, want32, f"cfg{cfg} valu fp32")
-    got16 = run(case, gpu, device, waves_per_block=4)
+    got16 = run(case, gpu, device, waves_per_block=4 | DECODE_VALU_TILE)
     e16 = assert_attention_close(got16, want32.to(torch.float16), f"cfg{cfg} valu fp16")
     log(f"decode: config {cfg} valu max-abs err fp32 {e32:.2e} fp16 {e16:.2e}")
 
 
 @pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (16, 1, 64)])
 @pytest.mark.parametrize("tps", [0, 96, 1024])
-def test_valu_tile_ragged_and_split(device, monkeypatch, hq, hkv, d, tps):
+def test_valu_tile_ragged_and_split(device, hq, hkv, d, tps):
     # Lengths with partial pages and partial 32-token tiles (1, 17, 33), a
     # full table row and one token short of it; one chunk, 3-tile chunks
     # (43 a sequence) and 32-tile chunks.
-    monkeypatch.setenv("IRIS_DECODE_KERNEL", "valu")
     lens = [1, 17, 33, 1000, 4095, 4096]
     log(f"decode valu: Hq={hq} Hkv={hkv} D={d} lens={lens} split={tps}")
     g = torch.Generator().manual_seed(hq + d + tps)
@@ -594,16 +591,15 @@ def test_valu_tile_ragged_and_split(device, monkeypatch, hq, hkv, d, tps):
     qg, btg, slg = to(device, q, bt, sl)
     cache = to(device, kd, vd, ks, vs)
     out = torch.empty(q.shape, dtype=torch.float32, device=device)
-    fused_int4_paged_decode_attention(qg, *cache, btg, slg, out, tokens_per_split=tps, waves_per_block=4)
+    fused_int4_paged_decode_attention(qg, *cache, btg, slg, out, tokens_per_split=tps, waves_per_block=4 | DECODE_VALU_TILE)
     torch.cuda.synchronize(device)
     assert_attention_close(out, want, f"valu Hq={hq} Hkv={hkv} D={d} split={tps}")
 
 
-def test_valu_tile_nan_poisoned_tails(device, monkeypatch):
+def test_valu_tile_nan_poisoned_tails(device):
     # As test_nan_poisoned_tails_do_not_leak, on the VALU tile.
-    monkeypatch.setenv("IRIS_DECODE_KERNEL", "valu")
     case, cpu, gpu = prepared(3, device)
-    clean = run(case, gpu, device, torch.float32, waves_per_block=4)
+    clean = run(case, gpu, device, torch.float32, waves_per_block=4 | DECODE_VALU_TILE)
     kd, vd, ks, vs = (t.clone() for t in cpu)
     g = torch.Generator().manual_seed(98)
     for b in range(case.config.batch):
@@ -616,6 +612,40 @@ def test_valu_tile_nan_poisoned_tails(device, monkeypatch):
         vd[last, tail] = torch.randint(0, 256, vd[last, tail].shape, dtype=torch.uint8, generator=g)
     ks[case.pad_page] = float("nan")
     vs[case.pad_page] = float("inf")
-    poisoned = run(case, to(device, kd, vd, ks, vs), device, torch.float32, waves_per_block=4)
+    poisoned = run(case, to(device, kd, vd, ks, vs), device, torch.float32, waves_per_block=4 | DECODE_VALU_TILE)
     assert torch.isfinite(poisoned).all()
     assert torch.equal(poisoned, clean)
+
+
+def test_recycled_workspace_block_is_zeroed(device):
+    # A caller's workspace tensor placed by the caching allocator where an
+    # earlier workspace was, after other data (0xFF bytes) passed through
+    # that block: the wrapper has never seen the new tensor, so it zero-fills
+    # its counter region, every merge runs, and the result is the checker's.
+    case, cpu, gpu = prepared(2, device)
+    if 2 not in _WANT:
+        _WANT[2] = eager_fp32(case, cpu)
+    q, bt, sl = to(device, case.query, case.block_table, case.seq_lens)
+    B, hq, d = q.shape
+    lens = case.seq_lens.tolist()
+    nbytes = decode_plan(B, hq, 8, d, bt.shape[1], sum(lens), max(lens))[3]
+    assert nbytes > 0
+    out = torch.empty(q.shape, dtype=torch.float32, device=device)
+    first = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    fused_int4_paged_decode_attention(q, *gpu, bt, sl, out, workspace=first)
+    torch.cuda.synchronize(device)
+    assert_attention_close(out, _WANT[2], "first workspace")
+    where = first.data_ptr()
+    del first
+    junk = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    junk.fill_(0xFF)
+    torch.cuda.synchronize(device)
+    del junk
+    second = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    if second.data_ptr() != where:  # (another block: the same test on the junk bytes themselves)
+        second.fill_(0xFF)
+    out.fill_(0.0)
+    fused_int4_paged_decode_attention(q, *gpu, bt, sl, out, workspace=second)
+    torch.cuda.synchronize(device)
+    log(f"decode: recycled workspace block, same address: {second.data_ptr() == where}")
+    assert_attention_close(out, _WANT[2], "recycled workspace")
