@@ -55,7 +55,9 @@ extern "C" {
  *   cos_cache, sin_cache [max_position, rotary_dim / 2] fp16
  *   k_data .. v_scale  the cache, written in place at the valid slots only
  *
- * head_dim must be a multiple of 64 and at most 512; rotary_dim even, in
+ * head_dim must be a multiple of 32 and at most 512 (the reference's fused
+ * kernel takes multiples of 64, fused_kv.py:636-637; its eager path any
+ * multiple of the group size); rotary_dim even, in
  * [0, head_dim] (a multiple of 16 keeps the vector RoPE path; other values
  * read each rotated dim's partner, cos and sin separately).  Like the reference
  * kernel, this function does not check slot or position ranges or duplicate
@@ -125,8 +127,9 @@ int iris_quantize_pack_int4(const void *x, void *packed, void *scales, int64_t n
  * the general kernel), and one of the selection bits below may be or-ed
  * in.  out_waves carries the wave count and the selection bit into the
  * launch, so a plan and its launch always run the same kernel.
- * max_pages counts 16-token pages: block_table columns * page_size / 16.
- * head_dim 64, 128 or 256; any num_q_heads / num_kv_heads.
+ * max_pages counts 16-token pages: ceil(block_table columns * page_size /
+ * 16), the tokens a row addresses.  head_dim any multiple of 32 up to 512;
+ * any num_q_heads / num_kv_heads.
  */
 /* Kernel selection bits of waves_per_block (no reference counterpart; for
  * A/B measurements and tests).  IRIS_DECODE_PAGE_KERNEL: 16-wave plans run
@@ -137,6 +140,14 @@ int iris_quantize_pack_int4(const void *x, void *packed, void *scales, int64_t n
  * head_dim 128, 16 at head_dim 64; other shapes are refused). */
 #define IRIS_DECODE_PAGE_KERNEL 0x100
 #define IRIS_DECODE_VALU_TILE 0x200
+/* IRIS_DECODE_ANY_KERNEL: the any-shape kernel, which takes every head_dim
+ * that is a multiple of 32 up to 512 and every page size, with fp32
+ * dequantisation as the eager path does it.  iris_decode_plan sets it by
+ * itself for head dims other than 64, 128 and 256; a caller whose page size
+ * is not 16 << k (16-256) must ask for it (the plan is not told the page
+ * size), and iris_int4_paged_decode_attention refuses such a page size
+ * without it.  At most one selection bit may be set. */
+#define IRIS_DECODE_ANY_KERNEL 0x400
 int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                      int64_t max_pages, int64_t total_tokens, int64_t max_tokens,
                      int32_t tokens_per_split, int32_t waves_per_block, int32_t *out_chunk_tiles,
@@ -180,11 +191,13 @@ int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, i
  *                max_chunks; past that the launch writes NaN into every
  *                output element rather than a wrong result)
  *
- * page_size 16 << k (16 to 256), head_dim 64, 128 or 256, and any
- * num_q_heads / num_kv_heads (the reference's fused path takes page_size 16,
- * head_dim 64 or 128 and at most 16 query heads per kv head,
- * fused_attention.py:390-403; its eager path takes any).  max_pages is the
- * number of block_table columns; plan with max_pages * page_size / 16.
+ * Any page_size >= 1, any head_dim that is a multiple of 32 up to 512, and
+ * any num_q_heads / num_kv_heads, as the eager path takes them
+ * (torch_eager_attention.py:72, :93; the reference's fused path takes
+ * page_size 16, head_dim 64 or 128 and at most 16 query heads per kv head,
+ * fused_attention.py:390-403).  Page sizes other than 16 << k (16-256)
+ * need a plan made with IRIS_DECODE_ANY_KERNEL.  max_pages is the number of
+ * block_table columns; plan with ceil(max_pages * page_size / 16).
  * Page ids and lengths are not
  * range-checked on the device (fused_attention.py:415-429 does that on the
  * host).  Tokens of the last page beyond seq_lens[b] are read but never

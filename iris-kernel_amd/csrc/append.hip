@@ -85,6 +85,7 @@ __global__ __launch_bounds__(256) void rope_int4_paged_append_kernel(
     int n_rows, int n_heads, double inv_heads, int head_dim, int rotary_dim) {
     constexpr int kRowsPerBlock = 256 / ROWLANES;
     const int chunks = head_dim >> 3;  // 8 dims per lane
+    const bool odd_groups = (head_dim >> 5) & 1;  // (head_dim 32, 96, 160, ...)
     const int lane = threadIdx.x & 63;
     const int c_raw = threadIdx.x & (ROWLANES - 1);
     const int c = c_raw < chunks ? c_raw : 0;  // padding lanes mirror chunk 0
@@ -203,7 +204,12 @@ __global__ __launch_bounds__(256) void rope_int4_paged_append_kernel(
             // D/2 bytes per row = chunks / 4 16-byte groups
             k_data[cache_row * (uint32_t)(chunks >> 2) + (c >> 2)] = kq;
             v_data[cache_row * (uint32_t)(chunks >> 2) + (c >> 2)] = vq;
-            if ((c & 7) == 0) {  // D/32 scales per row, two per 32-bit word
+            if (odd_groups) {
+                // An odd number of groups: rows of scales are 2-byte aligned,
+                // so each group's scale is a 16-bit store of its own.
+                reinterpret_cast<uint16_t*>(k_scale)[cache_row * (uint32_t)(head_dim >> 5) + (c >> 2)] = (uint16_t)ks;
+                reinterpret_cast<uint16_t*>(v_scale)[cache_row * (uint32_t)(head_dim >> 5) + (c >> 2)] = (uint16_t)vs;
+            } else if ((c & 7) == 0) {  // D/32 scales per row, two per 32-bit word
                 k_scale[(cache_row * (uint32_t)(head_dim >> 5) + (c >> 2)) >> 1] = ks2;
                 v_scale[(cache_row * (uint32_t)(head_dim >> 5) + (c >> 2)) >> 1] = vs2;
             }
@@ -223,7 +229,7 @@ extern "C" int iris_rope_int4_paged_append(
     (void)num_pages;
     (void)max_position;
     if (num_tokens < 0 || num_kv_heads <= 0 || page_size <= 0 || head_dim <= 0 ||
-        head_dim % 64 != 0 || head_dim > 512 || rotary_dim < 0 || rotary_dim > head_dim || rotary_dim % 2 != 0)
+        head_dim % 32 != 0 || head_dim > 512 || rotary_dim < 0 || rotary_dim > head_dim || rotary_dim % 2 != 0)
         return kInvalidArgument;
     if (num_tokens == 0) return kOk;
     // 32-bit row indices and the fp64 row -> (token, head) split: a launch

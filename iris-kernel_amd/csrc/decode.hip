@@ -64,6 +64,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "decode_any.h"
 #include "decode_mqa.h"
 #include "decode_pages.h"
 #include "iris_hip.h"
@@ -1368,20 +1369,29 @@ constexpr int64_t kPagesMinBytes = 100000000;  // K/V bytes above which the page
 // the GQA shapes of 7-70B models), over batches of similar lengths (its one
 // workgroup per CU balances ragged batches worse than the general kernel's
 // many small ones) that read at least kPagesMinBytes of K/V.
+// Shapes none of these kernels has -- head_dim other than 64, 128 or 256,
+// page sizes other than 16 << k -- run on the any-shape kernel
+// (decode_any.hip), named by a third bit, IRIS_DECODE_ANY_KERNEL: the plan
+// sets it for such head dims by itself; for such page sizes (which the
+// plan is not told) the caller asks for it, and a launch with such a page
+// size and no bit is refused.  The bit may also be asked for at any shape.
 constexpr int32_t kWaveMask = 0xFF;
 constexpr int32_t kPageKernel = IRIS_DECODE_PAGE_KERNEL;
 constexpr int32_t kValuTile = IRIS_DECODE_VALU_TILE;
-// The selection bits of waves_per_block, or -1 if it is not a valid request.
+constexpr int32_t kAnyKernel = IRIS_DECODE_ANY_KERNEL;
+// The selection bits of waves_per_block, or -1 if it is not a valid request
+// (at most one bit).
 static int32_t selection_of(int32_t waves_per_block) {
     if (waves_per_block < 0) return 0;  // (as 0: let the plan choose)
     const int32_t sel = waves_per_block & ~kWaveMask;
-    if ((sel & ~(kPageKernel | kValuTile)) != 0 || sel == (kPageKernel | kValuTile)) return -1;
+    if (sel != 0 && sel != kPageKernel && sel != kValuTile && sel != kAnyKernel) return -1;
     return sel;
 }
+static bool fast_head_dim(int64_t head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
 static int32_t waves_of(int32_t waves_per_block) { return waves_per_block < 0 ? 0 : waves_per_block & kWaveMask; }
 static bool pages_allowed(int32_t waves_per_block) {
     const int32_t w = waves_of(waves_per_block);
-    return (selection_of(waves_per_block) & kValuTile) == 0 && (w == 0 || w == pages_waves());
+    return (selection_of(waves_per_block) & (kValuTile | kAnyKernel)) == 0 && (w == 0 || w == pages_waves());
 }
 static bool pages_preferred(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                             int64_t total_tokens, int64_t max_tokens, bool lengths_known) {
@@ -1421,11 +1431,17 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
                                 int32_t waves_per_block, int32_t* out_chunk_tiles,
                                 int32_t* out_max_chunks, int32_t* out_waves,
                                 int64_t* out_workspace_bytes) {
-    if (batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
-        (head_dim != 64 && head_dim != 128 && head_dim != 256) || max_pages <= 0 || max_pages > 0x3FFFFFFF)
+    if (batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || !any_supported(head_dim) ||
+        max_pages <= 0 || max_pages > 0x3FFFFFFF)
         return kInvalidArgument;
     const int32_t sel = selection_of(waves_per_block);
     if (sel < 0) return kInvalidArgument;
+    if (sel == kAnyKernel || !fast_head_dim(head_dim)) {
+        const int st = any_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages * kPageSize, total_tokens,
+                                max_tokens, tokens_per_split, out_chunk_tiles, out_max_chunks, out_workspace_bytes);
+        if (st == kOk) *out_waves = any_waves() | kAnyKernel;
+        return st;
+    }
     // Unknown lengths (the sync-free positional handle): the widest batch
     // block_table admits stands in for them.
     const int64_t est_max = max_tokens < 0 ? max_pages * kPageSize : max_tokens;
@@ -1507,18 +1523,22 @@ extern "C" int iris_int4_paged_decode_attention(
     int64_t num_pages, int64_t max_pages, float softmax_scale, int32_t chunk_tiles,
     int32_t max_chunks, int32_t waves_per_block, void* stream) {
     (void)num_pages;
+    const int32_t sel = selection_of(waves_per_block);
+    if (sel < 0) return kInvalidArgument;
+    if (sel == kAnyKernel)
+        return any_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
+                          workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, page_size,
+                          max_pages, softmax_scale, chunk_tiles, max_chunks, stream);
     // page_size = 16 << shift: each table entry stands for 1 << shift
     // consecutive 16-token pages, so the kernels see max_pages << shift of
     // them per row (the count the plan was made with).
     int shift = 0;
     while (shift < 5 && (kPageSize << shift) != page_size) ++shift;
     if (shift == 5 || batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
-        (head_dim != 64 && head_dim != 128 && head_dim != 256) || max_pages <= 0 || (max_pages << shift) > 0x3FFFFFFF)
+        !fast_head_dim(head_dim) || max_pages <= 0 || (max_pages << shift) > 0x3FFFFFFF)
         return kInvalidArgument;
     const int64_t bt_cols = max_pages;
     max_pages <<= shift;
-    const int32_t sel = selection_of(waves_per_block);
-    if (sel < 0) return kInvalidArgument;
     const int32_t waves = waves_of(waves_per_block);
     if (waves == mqa_waves() && mqa_allowed(waves_per_block) &&
         mqa_supported(num_q_heads, num_kv_heads, head_dim) && chunk_tiles > 0)

@@ -31,6 +31,7 @@ SOURCES = {
     # the streaming kernel takes its prologue scalars in preloaded SGPRs
     "decode_stream.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=10"],
     "decode_mqa.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
+    "decode_any.hip": [],
     "decode_fp16.hip": [],
     "kv_fp16.hip": ["-ffp-contract=off"],
     "check.hip": [],

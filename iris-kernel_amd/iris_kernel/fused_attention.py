@@ -35,7 +35,7 @@ from . import _lib
 
 __all__ = ["fused_int4_paged_decode_attention", "_int4_paged_decode_attention", "decode_plan",
            "fused_fp16_paged_decode_attention", "_fp16_paged_decode_attention", "fp16_decode_plan",
-           "DECODE_PAGE_KERNEL", "DECODE_VALU_TILE"]
+           "DECODE_PAGE_KERNEL", "DECODE_VALU_TILE", "DECODE_ANY_KERNEL", "int4_decode_plan"]
 
 # Kernel selection bits or-ed into ``waves_per_block`` (IRIS_DECODE_PAGE_KERNEL
 # and IRIS_DECODE_VALU_TILE of include/iris_hip.h), for A/B measurements and
@@ -44,6 +44,10 @@ __all__ = ["fused_int4_paged_decode_attention", "_int4_paged_decode_attention", 
 # launch runs the kernel it planned.
 DECODE_PAGE_KERNEL = 0x100
 DECODE_VALU_TILE = 0x200
+# The any-shape kernel (IRIS_DECODE_ANY_KERNEL): every head_dim that is a
+# multiple of 32 up to 512, every page size.  The plan picks it by itself for
+# such head dims; page sizes other than 16 << k must ask for it.
+DECODE_ANY_KERNEL = 0x400
 
 
 def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, max_pages: int,
@@ -51,7 +55,9 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
                 waves_per_block: int = 0) -> tuple[int, int, int, int]:
     """(chunk_tiles, max_chunks, waves_per_block, workspace_bytes) from iris_decode_plan.
 
-    ``max_pages`` counts 16-token pages: block_table columns * page_size // 16."""
+    ``max_pages`` counts 16-token pages: ceil(block_table columns * page_size / 16).
+    For page sizes other than 16 << k, or ``head_dim`` other than 64, 128 and
+    256, use ``int4_decode_plan``, which asks for the any-shape kernel."""
     ct, mc, nw = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
     ws = ctypes.c_int64()
     status = _lib.lib().iris_decode_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages,
@@ -60,6 +66,24 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
                                          ctypes.byref(nw), ctypes.byref(ws))
     _lib.check(status, "iris_decode_plan")
     return ct.value, mc.value, nw.value, ws.value
+
+
+def _fast_page_size(page_size: int) -> bool:
+    """Page sizes the streaming, page and general kernels read: 16 << k, 16-256."""
+    return page_size in (16, 32, 64, 128, 256)
+
+
+def int4_decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
+                     bt_cols: int, total_tokens: int = -1, max_tokens: int = -1, tokens_per_split: int = 0,
+                     waves_per_block: int = 0) -> tuple[int, int, int, int]:
+    """The decode plan for a cache of ``page_size``-token pages and a block
+    table ``bt_cols`` columns wide: ``decode_plan`` over the tokens a row
+    addresses, with the any-shape kernel asked for when the page size is not
+    16 << k."""
+    if not _fast_page_size(page_size):
+        waves_per_block = (max(waves_per_block, 0) & 0xFF) | DECODE_ANY_KERNEL
+    return decode_plan(batch, num_q_heads, num_kv_heads, head_dim, -(-bt_cols * page_size // 16), total_tokens,
+                       max_tokens, tokens_per_split, waves_per_block)
 
 
 def _qk_scale(head_dim: int, softmax_scale) -> float:
@@ -178,9 +202,10 @@ def _launch_decode(query, k_data, v_data, k_scale, v_scale, block_table, seq_len
 
 # Scope of the INT4 decode beyond the reference's fused path (page_size 16,
 # head_dim 64/128, at most 16 query heads per kv head: fused_attention.py:
-# 390-403): pages of 16 << k tokens, head_dim 256, any GQA ratio.
-INT4_PAGE_SIZES = (16, 32, 64, 128, 256)
-INT4_HEAD_DIMS = (64, 128, 256)
+# 390-403): what its eager path takes (torch_eager_attention.py:72, :93) --
+# any page size, any head_dim that is a multiple of the 32-dim scale group
+# (up to 512), any GQA ratio.
+INT4_MAX_HEAD_DIM = 512
 
 
 def _validate_common_decode_inputs(query, block_table, seq_lens, *, num_pages: int,
@@ -196,13 +221,13 @@ def _validate_common_decode_inputs(query, block_table, seq_lens, *, num_pages: i
         raise ValueError("query must have shape [B, Hq, D]")
     if query.dtype != torch.float16:
         raise TypeError("query must use FP16(torch.float16)")
-    if page_size not in (INT4_PAGE_SIZES if int4 else (16,)):
+    if (page_size < 1) if int4 else (page_size != 16):
         raise NotImplementedError("decode fast path currently supports page_size="
-                                  + ("16 << k (16-256)" if int4 else "16"))
+                                  + ("any positive size" if int4 else "16"))
     batch, num_query_heads, head_dim = query.shape
-    if head_dim not in (INT4_HEAD_DIMS if int4 else (64, 128)):
+    if (head_dim % 32 or not 32 <= head_dim <= INT4_MAX_HEAD_DIM) if int4 else head_dim not in (64, 128):
         raise NotImplementedError("decode fast path currently supports head_dim in "
-                                  + ("{64, 128, 256}" if int4 else "{64, 128}"))
+                                  + ("multiples of 32 up to 512" if int4 else "{64, 128}"))
     if num_query_heads % num_kv_heads != 0:
         raise ValueError("num_query_heads must be divisible by num_kv_heads")
     if not int4 and num_query_heads // num_kv_heads > 16:
@@ -317,8 +342,8 @@ def fused_int4_paged_decode_attention(
     if batch == 0:
         return output
     scale = _qk_scale(head_dim, softmax_scale)
-    plan = decode_plan(batch, num_q_heads, num_kv_heads, head_dim, block_table.shape[1] * (page_size // 16),
-                       total, longest, tokens_per_split, waves_per_block)
+    plan = int4_decode_plan(batch, num_q_heads, num_kv_heads, head_dim, page_size, block_table.shape[1],
+                            total, longest, tokens_per_split, waves_per_block)
     _launch_decode(_dense(query, 16), k_data, v_data, k_scale, v_scale, block_table, seq_lens, output,
                    scale, plan, workspace)
     return output
@@ -338,8 +363,8 @@ def _int4_paged_decode_attention(query, k_data, v_data, k_scale, v_scale, block_
     if batch == 0:
         return
     scale = _qk_scale(head_dim, softmax_scale)
-    plan = decode_plan(batch, num_q_heads, k_data.shape[2], head_dim,
-                       block_table.shape[1] * (k_data.shape[1] // 16))
+    plan = int4_decode_plan(batch, num_q_heads, k_data.shape[2], head_dim, k_data.shape[1],
+                            block_table.shape[1])
     _launch_decode(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, scale,
                    plan)
 

@@ -89,10 +89,10 @@ def fused_rope_int4_paged_append(
     """RoPE(K), quantise K and V to group-32 INT4, pack, scatter into the pages.
 
     Bit-identical to ``torch_eager_append`` for the scope it accepts
-    (fp16, head_dim % 64 == 0, group_size == 32, any even rotary_dim <=
-    head_dim: the first rotary_dim dims of K are rotated, the rest pass
-    through, as the eager path does; the reference's fused kernel requires
-    rotary_dim == head_dim).
+    (fp16, head_dim a multiple of 32 up to 512, group_size == 32, any even
+    rotary_dim <= head_dim: the first rotary_dim dims of K are rotated, the
+    rest pass through, as the eager path does; the reference's fused kernel
+    requires head_dim % 64 == 0 and rotary_dim == head_dim).
     Slots < 0 are skipped.  Mutates k_data/v_data/k_scale/v_scale in place;
     the launch is asynchronous on the current stream.
     """
@@ -110,8 +110,10 @@ def fused_rope_int4_paged_append(
     if value.dtype != torch.float16:
         raise TypeError("value must use FP16(torch.float16)")
     num_tokens, num_kv_heads, head_dim = key.shape
-    if head_dim % 64 != 0:
-        raise NotImplementedError("Stage C currently requires head_dim divisible by 64")
+    # head_dim: every multiple of the 32-dim scale group up to 512, as the
+    # eager path takes it (the reference's fused path: multiples of 64).
+    if head_dim <= 0 or head_dim % 32 != 0 or head_dim > 512:
+        raise NotImplementedError("Stage C currently requires head_dim divisible by 32 (at most 512)")
     if group_size != 32:
         raise NotImplementedError("Stage C currently supports group_size=32")
     # Partial RoPE is accepted (the eager path's rule, torch_eager_kv.py:35-49,

@@ -39,7 +39,7 @@ def test_library_exports_every_declared_symbol():
 def test_append_rejects_unsupported_head_dim_before_launch():
     lib = _lib.lib()
     null = None
-    for d in (96, 0, 576):
+    for d in (80, 0, 576):  # a multiple of 32 up to 512
         st = lib.iris_rope_int4_paged_append(null, null, null, null, null, null, null, null, null,
                                              null, 4, 2, d, d, 16, 8, 16, null)
         assert st == 1
@@ -62,11 +62,21 @@ def test_decode_rejects_unsupported_shapes_before_launch():
                                                     null, 0, a["B"], a["Hq"], a["Hkv"], a["D"], a["P"],
                                                     a["NP"], a["maxP"], ctypes.c_float(0.1), a["ct"],
                                                     a["mc"], a["nw"], null)
-    assert call(P=48) == 1          # page_size must be 16 << k
+    assert call(P=48) == 1          # page_size must be 16 << k (without the any-shape bit)
     assert call(P=8) == 1
     assert call(P=512) == 1
-    assert call(D=96) == 1          # head_dim in {64, 128, 256}
+    assert call(D=96) == 1          # head_dim in {64, 128, 256} (without the any-shape bit)
     assert call(D=512) == 1
+    # the any-shape kernel: any page size, head_dim a multiple of 32 up to 512
+    any_ = 4 | 0x400
+    assert call(P=48, D=96, nw=any_, ct=6, mc=1) == 2      # valid: it gets as far as the launch
+    assert call(P=0, nw=any_) == 1                          # page_size >= 1
+    assert call(D=80, nw=any_) == 1                         # multiple of 32
+    assert call(D=544, nw=any_) == 1                        # at most 512
+    assert call(P=48, nw=any_, ct=2, mc=2) == 1             # chunks do not cover 4 x 48 tokens
+    assert call(P=48, nw=any_, ct=3, mc=4) == 1             # chunks of whole 64-token tiles
+    assert call(P=48, nw=any_, ct=2, mc=3) == 3             # three chunks need a workspace
+    assert call(nw=0x400 | 0x100) == 1                      # one selection bit at most
     assert call(Hq=9) == 1          # Hq not divisible by Hkv
     assert call(ct=1, mc=1) == 1    # chunks do not cover max_pages
     assert call(nw=5) == 1
@@ -213,8 +223,29 @@ def test_decode_plan_overrides_and_errors():
     assert ws == pages_workspace(2, 8, 128, 16)
     # ... and falls back to the general kernel where it has no layout (Hkv=3)
     assert decode_plan(2, 9, 3, 128, 64, waves_per_block=16)[2] == 4
-    with pytest.raises(RuntimeError):
-        decode_plan(2, 8, 2, 96, 64)
+    # head dims other than 64 / 128 / 256 plan the any-shape kernel by themselves
+    ct, mc, nw, ws = decode_plan(2, 8, 2, 96, 64, tokens_per_split=256)
+    assert (ct, mc, nw) == (8, 4, 4 | 0x400), (ct, mc, nw)
+    assert ws == any_workspace(2, 8, 96, 4)
+    assert decode_plan(2, 8, 2, 512, 64)[2] == 4 | 0x400
+    for bad in (80, 544, 0):
+        with pytest.raises(RuntimeError):
+            decode_plan(2, 8, 2, bad, 64)
+    # page sizes other than 16 << k: int4_decode_plan asks for the any-shape kernel
+    from iris_kernel.fused_attention import int4_decode_plan
+
+    assert int4_decode_plan(2, 8, 2, 128, 48, 10)[2] == 4 | 0x400
+    assert int4_decode_plan(2, 8, 2, 128, 1, 1000)[2] == 4 | 0x400
+    assert int4_decode_plan(2, 8, 2, 128, 32, 10)[2] in (4, 16)
+    ct, mc, nw, ws = int4_decode_plan(3, 8, 2, 128, 48, 10, tokens_per_split=64)
+    assert ct * 32 * mc >= 10 * 48 and ct % 2 == 0
+
+
+def any_workspace(batch, hq, d, max_chunks):
+    """Split-KV workspace of the any-shape kernel: counters, then o / l
+    [B][chunks][Hq][D] and (m, l) [B][chunks][Hq][2] fp32."""
+    up = lambda x: (x + 255) // 256 * 256
+    return up(batch * 512) + up(batch * max_chunks * hq * d * 4) + batch * max_chunks * hq * 2 * 4
 
 
 def test_decode_check_rejects_bad_arguments_before_launch():
@@ -258,7 +289,7 @@ def test_decode_kernel_selection_bits(monkeypatch):
     with pytest.raises(RuntimeError):
         decode_plan(*shape, waves_per_block=DECODE_PAGE_KERNEL | DECODE_VALU_TILE)
     with pytest.raises(RuntimeError):
-        decode_plan(*shape, waves_per_block=0x400)
+        decode_plan(*shape, waves_per_block=0x800)
 
 
 def test_valu_tile_selection_covers_two_layouts():

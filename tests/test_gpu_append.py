@@ -63,25 +63,48 @@ def test_config_append_bit_exact(device, cfg):
     assert_same(ref, gpu)
 
 
-@pytest.mark.parametrize("head_dim", [64, 128, 192, 256, 512])
-def test_head_dims_and_skipped_slots(device, head_dim):
-    # every supported head_dim (multiples of 64; 192 exercises padded lanes),
-    # an odd number of kv heads, random non-contiguous slots with skips
-    log(f"append: head_dim {head_dim}")
-    g = torch.Generator().manual_seed(head_dim)
-    T, H, NP = 37, 3, 6
+@pytest.mark.parametrize("head_dim,page_size", [(64, 16), (128, 16), (192, 16), (256, 16), (512, 16),
+                                                (32, 16), (96, 16), (160, 16), (224, 16), (480, 16),
+                                                (96, 1), (96, 48), (128, 8), (320, 48)])
+def test_head_dims_and_skipped_slots(device, head_dim, page_size):
+    # head dims that are multiples of 32 up to 512 (192 and 96 exercise
+    # padded lanes; an odd number of 32-dim groups -- 32, 96, 160, 224, 480 --
+    # stores each scale on its own, rows being 2-byte aligned), page sizes
+    # other than 16, an odd number of kv heads, random non-contiguous slots
+    # with skips
+    log(f"append: head_dim {head_dim} page_size {page_size}")
+    g = torch.Generator().manual_seed(head_dim + page_size)
+    T, H, NP = 37, 3, -(-96 // page_size)
+    P = page_size
     key = (torch.randn(T, H, head_dim, generator=g) * 3).to(torch.float16)
     value = torch.randn(T, H, head_dim, generator=g).to(torch.float16)
     pos = torch.randint(0, 50, (T,), generator=g, dtype=torch.int32)
-    slots = torch.randperm(NP * 16, generator=g)[:T].to(torch.int32)
+    slots = torch.randperm(NP * P, generator=g)[:T].to(torch.int32)
     slots[::5] = -1
     cos, sin = workloads.make_rope_cache(50, head_dim)
-    cache = (torch.zeros(NP, 16, H, head_dim // 2, dtype=torch.uint8),
-             torch.zeros(NP, 16, H, head_dim // 2, dtype=torch.uint8),
-             torch.full((NP, 16, H, head_dim // 32), -1.0, dtype=torch.float16),
-             torch.full((NP, 16, H, head_dim // 32), -1.0, dtype=torch.float16))
-    ref, gpu = run_both(device, key, value, pos, slots, cos, sin, cache, head_dim)
+    cache = (torch.zeros(NP, P, H, head_dim // 2, dtype=torch.uint8),
+             torch.zeros(NP, P, H, head_dim // 2, dtype=torch.uint8),
+             torch.full((NP, P, H, head_dim // 32), -1.0, dtype=torch.float16),
+             torch.full((NP, P, H, head_dim // 32), -1.0, dtype=torch.float16))
+    ref = tuple(t.clone() for t in cache)
+    gpu = to(device, *cache)
+    torch_eager_append(key, value, pos, slots, cos, sin, *ref, rotary_dim=head_dim, group_size=32, page_size=P)
+    fused_rope_int4_paged_append(*to(device, key, value, pos, slots, cos, sin), *gpu, rotary_dim=head_dim,
+                                 group_size=32, page_size=P)
+    torch.cuda.synchronize(device)
     assert_same(ref, gpu)
+
+
+@pytest.mark.parametrize("head_dim", [80, 544])
+def test_unsupported_head_dim_raises(device, head_dim):
+    # a multiple of the 32-dim group up to 512, else NotImplementedError
+    x = torch.zeros(2, 1, head_dim, dtype=torch.float16, device=device)
+    i = torch.zeros(2, dtype=torch.int32, device=device)
+    cache = (torch.zeros(1, 16, 1, head_dim // 2, dtype=torch.uint8, device=device),) * 2 + \
+            (torch.zeros(1, 16, 1, head_dim // 32, dtype=torch.float16, device=device),) * 2
+    cs = torch.zeros(4, head_dim // 2, dtype=torch.float16, device=device)
+    with pytest.raises(NotImplementedError):
+        fused_rope_int4_paged_append(x, x, i, i, cs, cs, *cache, rotary_dim=head_dim, group_size=32, page_size=16)
 
 
 def test_ties_subnormals_and_extremes(device):
@@ -201,7 +224,8 @@ def test_validation_errors(device, mutate, exc):
 @pytest.mark.parametrize("head_dim,rotary_dim", [
     (128, 0), (128, 16), (128, 64), (128, 96), (128, 112),   # multiples of 16: vector RoPE path
     (128, 2), (128, 6), (128, 34), (128, 100), (128, 126),   # per-element path
-    (64, 32), (64, 10), (256, 128), (256, 250), (512, 256)])
+    (64, 32), (64, 10), (256, 128), (256, 250), (512, 256),
+    (96, 96), (96, 48), (96, 10), (32, 32), (32, 6), (160, 64), (480, 480)])
 def test_partial_rotary_bit_exact(device, head_dim, rotary_dim):
     # Partial RoPE as the eager path defines it (torch_eager_kv.py:35-49):
     # the first rotary_dim dims rotate, the rest pass through.

@@ -14,7 +14,8 @@ the codes' +8 offset by a second sum, give NaN: both are non-finite.)
 
 Each case is run on the plan's own choice, on each INT4 kernel forced (the
 streaming kernel at its shape, the MQA kernel at its shape, the page kernel,
-the general kernel and its VALU tile), with one chunk a sequence and with
+the general kernel and its VALU tile, the any-shape kernel, which a head_dim
+of 96 selects by itself), with one chunk a sequence and with
 split-KV, and on a cache the package's own append wrote from an infinite key
 and value.  The FP16-cache decode gets the same check with NaN / Inf cache
 values."""
@@ -23,8 +24,8 @@ import torch
 
 from helpers import ATOL, log, to
 from iris_kernel import workloads
-from iris_kernel.fused_attention import (DECODE_PAGE_KERNEL, DECODE_VALU_TILE, fused_fp16_paged_decode_attention,
-                                         fused_int4_paged_decode_attention)
+from iris_kernel.fused_attention import (DECODE_ANY_KERNEL, DECODE_PAGE_KERNEL, DECODE_VALU_TILE,
+                                         fused_fp16_paged_decode_attention, fused_int4_paged_decode_attention)
 from iris_kernel.fused_kv import fused_rope_int4_paged_append
 from oracle.torch_eager_attention import (torch_eager_fp16_paged_decode_attention,
                                           torch_eager_int4_paged_decode_attention)
@@ -47,6 +48,9 @@ KERNELS = [
     ("mqa-pages", 16, 1, 64, 16 | DECODE_PAGE_KERNEL),
     ("mqa-general", 16, 1, 64, 4),
     ("mqa-valu", 16, 1, 64, 4 | DECODE_VALU_TILE),
+    ("gqa-any", 32, 8, 128, DECODE_ANY_KERNEL),
+    ("mqa-any", 16, 1, 64, DECODE_ANY_KERNEL),
+    ("d96-any", 8, 2, 96, 0),
 ]
 
 # (name, what is poisoned): sequence b, token t < L_b, kv head, scale group.
