@@ -114,14 +114,13 @@ inline int64_t counter_region_bytes(int64_t batch) { return (batch * kCountersPe
 // An acquire-release arrival (what the HIP memory model prescribes) makes
 // the compiler add buffer_wbl2 sc1 before it and buffer_inv sc1 after it: a
 // write-back of the whole L2 and an invalidation of it, which these accesses
-// do not need.  On MI355X that costs 1.2-2 us per cfg2 decode launch
-// (38.7 against 40.3 us, A/B on one box).  Building with
-// -DIRIS_ARRIVE_ORDER=__ATOMIC_ACQ_REL restores the fenced form.
-#ifndef IRIS_ARRIVE_ORDER
-#define IRIS_ARRIVE_ORDER __ATOMIC_RELAXED
-#endif
+// do not need.  On MI355X that cost 1.2-2 us per cfg2 decode launch
+// (38.7 against 40.3 us, A/B on one box).  The order this argument needs in
+// the emitted code -- stores waited for and a barrier before the arrival, the
+// merge's loads after its returned count and a barrier -- is checked on every
+// decode kernel's gfx950 code by tests/test_isa_split_kv_order.py.
 __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expect) {
-    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, IRIS_ARRIVE_ORDER, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = old + 1 == expect;
     if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return last;

@@ -132,3 +132,51 @@ def vmem_sgpr_hazards(lines: list[str]) -> list[tuple[str, int]]:
             if dst:
                 recent.append((dst, 0))
     return found
+
+
+_RET_ATOMIC = re.compile(r"^(global|buffer|flat)_atomic_\S+\s.*\bsc0\b")
+_SC1_STORE = re.compile(r"^(global|buffer|flat)_store\S*\s.*\bsc1\b")
+_SC1_LOAD = re.compile(r"^(global|buffer|flat)_load\S*\s.*\bsc1\b")
+_VMCNT0 = re.compile(r"^s_waitcnt\s.*\bvmcnt\(0\)")
+
+
+def _instructions(lines: list[str]) -> list[str]:
+    out = []
+    for raw in lines:
+        text = raw.split(";")[0].strip()
+        if text and not text.startswith(".") and not text.endswith(":"):
+            out.append(text)
+    return out
+
+
+def split_kv_order(lines: list[str]) -> tuple[list[str], int]:
+    """The split-KV arrival protocol in a kernel's instructions (layout
+    order).  For every returning atomic (an arrival): the device-coherent
+    (sc1) partial stores before it must be complete -- an s_waitcnt
+    vmcnt(0) and a workgroup barrier between the last of them and the
+    atomic -- and the first sc1 load after it (a merge reading the
+    partials) must come after an s_waitcnt vmcnt(0) (the atomic's returned
+    count) and a barrier (its broadcast to the workgroup).  Returns the
+    violations and the number of (arrival, merge load) pairs checked."""
+    ins = _instructions(lines)
+    bad, pairs = [], 0
+    for i, t in enumerate(ins):
+        if not _RET_ATOMIC.match(t):
+            continue
+        stores = [j for j in range(i) if _SC1_STORE.match(ins[j])]
+        if stores:
+            between = ins[stores[-1] + 1:i]
+            if not any(_VMCNT0.match(x) for x in between) or "s_barrier" not in between:
+                bad.append(f"arrival '{t}' not preceded by a wait and a barrier after '{ins[stores[-1]]}'")
+        load = next((k for k in range(i + 1, len(ins)) if _SC1_LOAD.match(ins[k])), None)
+        if load is not None:
+            pairs += 1
+            between = ins[i + 1:load]
+            if not any(_VMCNT0.match(x) for x in between) or "s_barrier" not in between:
+                bad.append(f"merge load '{ins[load]}' issued before the arrival '{t}' returned")
+    return bad, pairs
+
+
+def kernel_symbols(asm: str) -> list[str]:
+    """Names of the kernel functions in an assembly listing."""
+    return re.findall(r"^\s*\.type\s+(\S+),@function", asm, flags=re.M)

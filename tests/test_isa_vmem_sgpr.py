@@ -3,35 +3,8 @@ an SGPR that a VALU instruction wrote fewer than 5 wait states earlier (see
 isa_hazards.vmem_sgpr_hazards).  The kernels issue some loads as inline
 assembly, which the compiler does not pad; a descriptor restored with
 v_readfirstlane right before such a load would address the wrong memory.
-Compiles every source once (about a minute); runs without a GPU."""
-import shutil
-import subprocess
-from pathlib import Path
-
-import pytest
-
+Uses the session's gfx950 assembly of every source; runs without a GPU."""
 from isa_hazards import vmem_sgpr_hazards
-from iris_kernel import _build
-
-
-@pytest.fixture(scope="module")
-def asm_by_source(tmp_path_factory):
-    try:
-        hipcc = _build._hipcc()
-    except RuntimeError:
-        pytest.skip("hipcc not available")
-    if shutil.which(hipcc) is None and not Path(hipcc).exists():
-        pytest.skip("hipcc not available")
-    out_dir = tmp_path_factory.mktemp("isa_sgpr")
-    result = {}
-    for src, extra in _build.SOURCES.items():
-        out = out_dir / (Path(src).stem + ".s")
-        cmd = [hipcc, *_build._common_flags(), *extra, "--cuda-device-only", "-S", str(_build.CSRC / src),
-               "-o", str(out)]
-        proc = subprocess.run(cmd, capture_output=True, text=True)
-        assert proc.returncode == 0, proc.stderr[-2000:]
-        result[src] = out.read_text()
-    return result
 
 
 def test_no_vmem_reads_an_sgpr_right_after_a_valu_write(asm_by_source):
