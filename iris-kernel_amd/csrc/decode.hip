@@ -1456,7 +1456,8 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
          pages_preferred(batch, num_q_heads, num_kv_heads, head_dim, est_total, est_max,
                          total_tokens >= 0 && max_tokens >= 0))) {
         const int st = pages_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, total_tokens, max_tokens,
-                                  tokens_per_split, out_chunk_tiles, out_max_chunks, out_waves, out_workspace_bytes);
+                                  tokens_per_split, (sel & kPageKernel) == 0, out_chunk_tiles, out_max_chunks,
+                                  out_waves, out_workspace_bytes);
         if (st == kOk) *out_waves |= sel & kPageKernel;
         return st;
     }

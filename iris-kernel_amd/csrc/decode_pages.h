@@ -18,9 +18,11 @@ IRIS_INTERNAL bool pages_supported(int64_t num_q_heads, int64_t num_kv_heads, in
 // uses at most 4, so waves_per_block tells the two apart).
 IRIS_INTERNAL int pages_waves();
 
+// allow_stream: a plan for the streaming kernel where it covers the shape
+// (its launch will run it), else for this kernel.
 IRIS_INTERNAL int pages_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                              int64_t max_pages, int64_t total_tokens, int64_t max_tokens, int32_t tokens_per_split,
-                             int32_t* out_chunk_tiles, int32_t* out_max_chunks, int32_t* out_waves,
+                             bool allow_stream, int32_t* out_chunk_tiles, int32_t* out_max_chunks, int32_t* out_waves,
                              int64_t* out_workspace_bytes);
 
 IRIS_INTERNAL int64_t pages_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t max_chunks);

@@ -1090,8 +1090,8 @@ bool pages_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim
 int pages_waves() { return kWaves; }
 
 int pages_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t max_pages,
-               int64_t total_tokens, int64_t max_tokens, int32_t tokens_per_split, int32_t* out_chunk_tiles,
-               int32_t* out_max_chunks, int32_t* out_waves, int64_t* out_workspace_bytes) {
+               int64_t total_tokens, int64_t max_tokens, int32_t tokens_per_split, bool allow_stream,
+               int32_t* out_chunk_tiles, int32_t* out_max_chunks, int32_t* out_waves, int64_t* out_workspace_bytes) {
     const int hkv = (int)num_kv_heads, g = (int)(num_q_heads / num_kv_heads);
     const pg::PageGeom geo = pg::page_geom(hkv, (int)head_dim);
     const int64_t cap_tokens = max_pages * pg::kPageSize;
@@ -1101,6 +1101,14 @@ int pages_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t
     const int64_t max_tiles = (cap_tokens + pg::kTile - 1) / pg::kTile;
     const int64_t longest_tiles = (max_tokens + pg::kTile - 1) / pg::kTile;
     if (known && tokens_per_split <= 0 && total_tokens < batch * max_tokens) {
+        // The streaming kernel's shape runs its own balanced mode (one range
+        // a CU, a workgroup walking every piece of its range).
+        if (allow_stream && stream_supported(num_q_heads, num_kv_heads, head_dim) &&
+            stream_balanced_plan(batch, num_q_heads, head_dim, total_tokens, out_chunk_tiles, out_max_chunks,
+                                 out_workspace_bytes) == kOk) {
+            *out_waves = kWaves;
+            return kOk;
+        }
         // Ragged lengths (known): the balanced mode.  The tiles of all
         // sequences laid end to end, at most tiles_ub of them, in W equal
         // ranges of at least four stages, each within the page-id window.

@@ -15,6 +15,13 @@ IRIS_INTERNAL bool stream_supported(int64_t num_q_heads, int64_t num_kv_heads, i
 // Most chunks per sequence a launch can merge.
 IRIS_INTERNAL int stream_max_chunks();
 
+// Balanced-mode plan for ragged lengths (total_tokens known): about one
+// range of the sequences' tiles, plus a per-sequence start cost, a CU;
+// chunk_tiles negative (minus the units a range holds at most).
+IRIS_INTERNAL int stream_balanced_plan(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t total_tokens,
+                                       int32_t* out_chunk_tiles, int32_t* out_max_chunks,
+                                       int64_t* out_workspace_bytes);
+
 // Split-KV workspace of a launch with max_chunks chunks per sequence.
 IRIS_INTERNAL int64_t stream_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim,
                                              int64_t max_chunks);

@@ -70,9 +70,23 @@ constexpr int kJobs = 3;            // loads per wave per slot
 constexpr int kMaxChunkTiles = 64;  // a chunk's 128 page ids fill two VGPRs
 constexpr int kMaxChunks = 64;      // partials the merge reads
 constexpr int kMergeBatch = 8;      // partials in flight per thread in the merge
-constexpr int kMergeGroup = 8;      // chunks merged by the last of each group (two levels past 8)
+// Chunks merged by the last of each group (two levels past 32): one merge
+// reads a partial in about 0.1 us past its ~1.2 us latency, a second level
+// costs a publish, an arrival and another merge's latency, so one level is
+// the faster up to about 32 partials (configuration 3: up to 20 a sequence).
+constexpr int kMergeGroup = 32;
 constexpr int kMaxGroups = 64;      // groups merged by the last group
 constexpr int kSeqCounter = kCountersPerSeq - 1;  // a sequence's group-level arrival counter
+// Balanced mode: what starting a piece costs, in 32-token tiles of
+// streaming (the epilogue, publish and arrival of the piece before, the
+// page-id round trip and the ring's fill: about 4.6 us at 1.25 us a tile),
+// charged to every sequence when the ranges are cut.  Configuration 3
+// (interleaved A/B on one box): 53.3 us at 3, 52.1 at 4, 51.8 at 5.
+constexpr int kPieceCost = 5;
+// Pieces one range can meet: a range has at most kMaxChunkTiles units, and
+// every piece but the first takes at least kPieceCost + 1 of them.
+constexpr int kMaxPieces = 40;
+static_assert(kMaxChunkTiles / (kPieceCost + 1) + 2 <= kMaxPieces, "the piece list of a range");
 static_assert(kMaxGroups < kSeqCounter, "group counters and the sequence counter share a sequence's region");
 constexpr float kLazy = 2.0f;       // rescale when a row maximum grows by more (base 2)
 constexpr int kSC1 = 16;            // cache-policy bit sc1: device-coherent access
@@ -102,7 +116,9 @@ struct Geo {
     // The empty scale-load slot of waves 4-15 writes (zeros) here.
     static constexpr int SINK_OFF = P_OFF + HKV * P_AREA;
     static constexpr int EPI_AREA = (8 + GQ * D) * 4;  // one set's (m, l, o) of a kv head in the epilogue
-    static constexpr int LDS_MAIN = SINK_OFF + 1024;
+    // The balanced mode's piece list (the ring, P areas and sink stay clear of it).
+    static constexpr int LIST_OFF = SINK_OFF + 1024;
+    static constexpr int LDS_MAIN = LIST_OFF + (6 * kMaxPieces + 4) * 4;
 };
 
 struct Args {
@@ -291,56 +307,596 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
     const int jq = lane >> 4;  // MFMA k-chunk (A, B) or row quad (C)
     const int kvh = wave % HKV, par = wave / HKV;  // kv head; tiles of this parity
 
-    // ---- this workgroup's piece of work: sequence b, tiles [t_begin, t_end),
-    // its chunk index and the sequence's chunk count, the slot of its chunk 0.
-    // Chunk mode (p_chunk_tiles > 0): (b, chunk) = (wg / max_chunks, wg %
-    // max_chunks), tiles chunk * chunk_tiles .. (the chunks of a sequence
-    // on one XCD).  Balanced mode (p_chunk_tiles < 0, ragged batches): the
-    // sequences' tiles laid end to end (T in all) are cut into W =
-    // max_chunks equal ranges [w T / W, (w + 1) T / W); a sequence is cut
-    // where the ranges meet it; workgroup w < W takes the piece holding its
-    // range's first tile, workgroup W + b sequence b's first piece when b
-    // starts inside a range.  So every piece has one workgroup and each
-    // workgroup one piece.
+    // ---- the pieces of work: sequence b, tiles [t_begin, t_end), the
+    // piece's chunk index in its sequence and the sequence's chunk count, the
+    // slot of its chunk 0.  Chunk mode (p_chunk_tiles > 0): one piece a
+    // workgroup, (b, chunk) = (wg / max_chunks, wg % max_chunks), tiles
+    // chunk * chunk_tiles .. (the chunks of a sequence on one XCD).
+    // Balanced mode (p_chunk_tiles < 0, ragged batches): every sequence
+    // stands for its tiles plus kPieceCost units (what starting a piece
+    // costs: the page-id round trip, the ring's fill, the epilogue); the
+    // units of all sequences laid end to end (C in all) are cut into W =
+    // max_chunks equal ranges [w C / W, (w + 1) C / W), one a workgroup, and
+    // a workgroup computes, one after the other, every piece of a sequence
+    // whose tiles meet its range.  Chunk c of sequence b is the piece in the
+    // c-th range its tiles meet; it owns workspace slot w + b (unique: the
+    // ranges of a later sequence never come before an earlier one's).
     constexpr bool segmented = SEG;  // (the sign of p_chunk_tiles, a template parameter so chunk mode carries no scan)
-    int b, chunk, t_begin, t_lim = 0, seg_chunks = 0;
-    int64_t row0;
+    auto run_piece = [&](const int b, const int chunk, const int t_begin, const int t_lim, const int seg_chunks,
+                         const int64_t row0) __attribute__((always_inline)) {
+        const int share = segmented ? -p_chunk_tiles : p_chunk_tiles;
+        const int p0 = 2 * t_begin;
+        const int seq_len = p_seq_lens[b];
+
+        // ---- page ids of the chunk (logical page p0 + i in lane i of pid0 /
+        // pid1) and the raw query rows: neither depends on the sequence length,
+        // so they are in flight together with its load.
+        const int32_t* bt = p_block_table + (int64_t)b * p_bt_cols;
+        // (every lane loads, clamped into the table; no divergent branches
+        // around the loads, so none waits for another)
+        int pid0 = virtual_page(bt, min(p0 + lane, p_max_pages - 1), p_page_shift);
+        int pid1 = virtual_page(bt, min(p0 + 64 + lane, p_max_pages - 1), p_page_shift);
+        // Query A operand: row n = (h, g) = (n >> 2, n & 3), nonzero only where
+        // g == jq: 32 dims of group jq of head h.
+        const half_t* qh = p_q + ((int64_t)b * p_n_q_heads + kvh * GQ) * D;
+        u32x4_t qraw[4];
+        {
+            const half_t* qrow = qh + (n >> 2) * D + 32 * jq;
+    #pragma unroll
+            for (int m = 0; m < 4; ++m) qraw[m] = *reinterpret_cast<const u32x4_t*>(qrow + 8 * m);
+        }
+        asm volatile("" ::: "memory");  // keeps the loads above issued before the early return below
+
+        const int n_tiles = (seq_len + kTile - 1) / kTile;
+        if (t_begin >= n_tiles) return;  // uniform over the workgroup
+        const int t_end = segmented ? t_lim : min(t_begin + share, n_tiles);
+        const int n_stages = t_end - t_begin;
+        const int n_chunks = segmented ? seg_chunks : (n_tiles + share - 1) / share;
+        const int last_lp = (seq_len + kPage - 1) / kPage - 1;
+
+        // ---- this wave's three loads of a slot (the same every step); each
+        // fills 1 KiB of the slot, its lanes fetching the page chunks the
+        // swizzles put there:
+        // * K piece `wave` of tile s: page kr, token rows 2 qq and 2 qq + 1;
+        // * V piece `wave` of tile s - 1, the same rows;
+        // * waves 0-3: scales KS p0, KS p1 (tile s), VS p0, VS p1 (tile s - 1);
+        //   waves 4-15: an empty load into the sink.
+        const int kr = wave / PER_PAGE, qq = wave % PER_PAGE;
+        uint32_t k_voff, v_voff, s_voff;
+        {
+            const int P = qq * 64 + lane, row = P / CK, cpos = P % CK;
+            k_voff = (uint32_t)(row * CK + (cpos ^ kkey(row, kr))) * 16;
+            v_voff = (uint32_t)(row * CK + (cpos ^ vswz<CK>(16 * kr + row))) * 16;
+            const int srow = lane >> 2, scol = lane & 3;
+            s_voff = (uint32_t)(srow * 64 + ((scol ^ ((srow >> 2) & 3)) * 16));
+        }
+        const bool s_job = wave < 4;
+        const bool s_is_v = (wave & 2) != 0;
+        const int s_r = wave & 1;
+
+        // Physical page of logical page lp (past the sequence: its last page).
+        auto page_of = [&](int lp) -> int64_t {
+            const int rel = min(lp, last_lp) - p0;
+            return (int64_t)__builtin_amdgcn_readlane(rel < 64 ? pid0 : pid1, rel & 63);
+        };
+        pid0 = (int)opaque((uint32_t)pid0);
+        pid1 = (int)opaque((uint32_t)pid1);
+
+        // Slot of step s: K of tile s, V of tile s - 1.  Halves outside the
+        // chunk load with zero-size descriptors (no memory access; the load still
+        // writes zeros into its LDS bytes), so every wave has kJobs loads of every
+        // slot in flight.
+        auto issue = [&](int s) __attribute__((always_inline)) {
+            uint8_t* const dst = smem + (s & (kSlots - 1)) * SLOT;
+            const bool kv = s < n_stages;
+            const bool vv = s >= 1 && s <= n_stages;
+            const int64_t kp = kv ? page_of(2 * (t_begin + s) + kr) : 0;
+            const int64_t vp = vv ? page_of(2 * (t_begin + s - 1) + kr) : 0;
+            const bool sv = s_job && (s_is_v ? vv : kv);
+            const int64_t sp = sv ? page_of(2 * (t_begin + s - (s_is_v ? 1 : 0)) + s_r) : 0;
+            // (the page sizes are the kernel-scope constants: L::KPAGE named in
+            // these descriptor expressions makes clang drop the kernel's host
+            // launch stub)
+            const auto krs = buf_rsrc(a.k_data + kp * KPAGE, kv ? KPAGE : 0u);
+            const auto vrs = buf_rsrc(a.v_data + vp * KPAGE, vv ? KPAGE : 0u);
+            const auto srs = buf_rsrc((s_is_v ? a.v_scale : a.k_scale) + sp * SPAGE, sv ? SPAGE : 0u);
+            uint8_t* const kdst = dst + L::K_OFF + 1024 * wave;
+            uint8_t* const vdst = dst + L::V_OFF + 1024 * wave;
+            uint8_t* const sdst = s_job ? dst + L::KS_OFF + 1024 * wave : smem + L::SINK_OFF;
+            const uint32_t ko = k_voff, vo = v_voff, so = s_voff;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (IRIS_LDS void*)kdst, 16, ko, 0, 0, kNT);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (IRIS_LDS void*)vdst, 16, vo, 0, 0, kNT);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (IRIS_LDS void*)sdst, 16, so, 0, 0, kNT);
+        };
+        // The first kAhead + 1 slots stream in while the query operands are
+        // prepared (one slot more than the steady state keeps in flight: the
+        // deeper first queue measured 0.2-0.3 us faster at cfg2, a fourth slot
+        // and a single one slower).
+    #pragma unroll
+        for (int s = 0; s <= kAhead; ++s) issue(s);
+
+        half8_t qa[4];
+        {
+            const bool mine = (n & 3) == jq;
+    #pragma unroll
+            for (int m = 0; m < 4; ++m) qa[m] = q_operand(mine ? qraw[m] : u32x4_t{0, 0, 0, 0});
+        }
+        // Accumulator start that removes the +8 of the K codes: C row (h, g)
+        // gets -8 * 2^-24 * (sum of q over group g of head h, as the A operand
+        // holds it, high-nibble dims / 16 counted 16 times).  Lane (4 h + g, g)
+        // holds that group in qa; C lane (n, jq) needs rows (jq, 0..3).
+        float4_t init;
+        {
+            float part = 0.0f;
+    #pragma unroll
+            for (int m = 0; m < 4; ++m)
+    #pragma unroll
+                for (int i = 0; i < 8; ++i) part += (float)qa[m][i] * ((i & 2) ? 16.0f : 1.0f);
+            part *= -8.0f * 5.9604644775390625e-08f;
+    #pragma unroll
+            for (int g = 0; g < 4; ++g)
+                init[g] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                       4 * (16 * g + 4 * jq + g), __builtin_bit_cast(int, part)));
+        }
+
+        // ---- per-lane LDS offsets within a slot
+        // K operand of chain e: token T = 16 (n >> 3) + 4 ((n & 7) >> 1) + (n & 1) + 2 e,
+        // 16 bytes = dims [32 jq, 32 jq + 32) of head kvh.
+        const int T0 = 16 * (n >> 3) + 4 * ((n & 7) >> 1) + (n & 1);
+        uint32_t k_off[2], ks_off[2], vs_off[2];
+    #pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int T = T0 + 2 * e;
+            const int r = T >> 4, row = T & 15;
+            k_off[e] = (uint32_t)(L::K_OFF + r * L::KPAGE + (row * CK + ((kvh * 4 + jq) ^ kkey(row, r))) * 16);
+            const int srow = row * 64 + (((kvh >> 1) ^ ((row >> 2) & 3)) * 16) + (kvh & 1) * 8;
+            ks_off[e] = (uint32_t)(L::KS_OFF + r * L::SPAGE + srow);
+            vs_off[e] = (uint32_t)(L::VS_OFF + r * L::SPAGE + srow);
+        }
+        // Transposed V reads of group g: lane (n, jq) points at token tr_tok's
+        // 8-byte half (n & 1) of group g's chunk; after the 8 x 8 byte transpose
+        // it holds byte column n of 8 tokens (k-slot order of v_operands).
+        uint32_t tr_off[G];
+        {
+            const int trk = n >> 1;
+            const int tr_tok = 4 * jq + (trk & 3) + 16 * (trk >> 2);
+    #pragma unroll
+            for (int g = 0; g < G; ++g)
+                tr_off[g] = (uint32_t)(L::V_OFF + (tr_tok >> 4) * L::KPAGE +
+                                       ((tr_tok & 15) * CK + ((kvh * 4 + g) ^ vswz<CK>(tr_tok))) * 16 + 8 * (n & 1));
+        }
+        // P area of the kv head: row (h, g) = 4 h + g, 32 halves in k-slot order
+        // of the tile's token blocks (block jq' = tokens 4 jq' + i of both
+        // pages).  Lane (n, jq) writes tokens T0 and T0 + 2, k-slots
+        // 4 (n >> 3) + 2 (n & 1) and the next, of block (n & 7) >> 1 in rows
+        // (jq, 0..3); it reads row n, block jq (rows (h, g) feed the PV of group
+        // g only: the other groups' rows carry the wrong V scale and their C rows
+        // are discarded).
+        const uint32_t p_base = lds_addr(smem + L::P_OFF + kvh * L::P_AREA);
+        const uint32_t p_wr =
+            p_base + (uint32_t)((jq * 4) * L::P_ROW + (((n & 7) >> 1) * 8 + 4 * (n >> 3) + 2 * (n & 1)) * 2);
+        const uint32_t p_rd = p_base + (uint32_t)(n * L::P_ROW + jq * 16);
+
+        const float c24 = a.log2_scale * 16777216.0f;  // MFMA units -> base-2 logits
+        float m_run = -INFINITY;                       // row maximum, base-2 logits
+        float l_part = 0.0f;
+        float ps[G];  // sums of the PV weights per group (V code offset)
+        float4_t o[G][2];
+    #pragma unroll
+        for (int g = 0; g < G; ++g) {
+            ps[g] = 0.0f;
+            o[g][0] = o[g][1] = float4_t{0, 0, 0, 0};
+        }
+        float t[2];     // scores (base-2 logits) of tokens T0, T0 + 2: first half -> second half
+        float mx = 0.0f;  // their row maximum
+
+        // First half of tile `stage` (K half of its slot): scores of the lane's
+        // two tokens and the row maximum.  The two QK chains are interleaved.
+        auto first_half = [&](int stage, uint32_t base) __attribute__((always_inline)) {
+            const int tok0 = (t_begin + stage) * kTile;
+            u32x4_t kq[2];
+            u32x2_t ksc[2];
+            lds_tile_reads(base + k_off[0], base + k_off[1], base + ks_off[0], base + ks_off[1], kq[0], kq[1], ksc[0],
+                           ksc[1]);
+            float4_t acc[2] = {init, init};
+    #pragma unroll
+            for (int e = 0; e < 2; ++e)
+    #pragma unroll
+                for (int m = 0; m < 4; ++m) acc[e] = mfma16x16x32(qa[m], k_operand(kq[e][m]), acc[e]);
+    #pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const half2_t k01 = as_half2(ksc[e][0]), k23 = as_half2(ksc[e][1]);
+                float s = (float)k01.x * acc[e][0];
+                s = __builtin_fmaf((float)k01.y, acc[e][1], s);
+                s = __builtin_fmaf((float)k23.x, acc[e][2], s);
+                s = __builtin_fmaf((float)k23.y, acc[e][3], s);
+                // base-2 logit; s - s is 0 for a finite score and NaN for +-inf,
+                // so a non-finite K scale or query gives NaN as the eager
+                // dequantisation does, never a -inf that would drop the token
+                t[e] = __builtin_fmaf(s, c24, s - s);
+            }
+            if (tok0 + kTile > seq_len) {
+    #pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    if (tok0 + T0 + 2 * e >= seq_len) t[e] = -INFINITY;
+            }
+            // row jq = head jq; its maximum is finite (token tok0 < seq_len)
+            mx = row16_max(__builtin_elementwise_maximum(t[0], t[1]));
+        };
+
+        // Second half of tile `stage` (V half of the next slot): online softmax
+        // (lazy rescale), PV weights w = p * v_scale (one fp16 rounding), tokens
+        // T0 and T0 + 2 packed per group, and the PV products.
+        auto second_half = [&](int stage, uint32_t base) __attribute__((always_inline)) {
+            const int tok0 = (t_begin + stage) * kTile;
+            u32x2_t vsc[2];
+            int2v_t vw[G];
+            uint32_t tra[G];
+    #pragma unroll
+            for (int g = 0; g < G; ++g) tra[g] = base + tr_off[g];
+            lds_v_reads(base + vs_off[0], base + vs_off[1], tra, vsc[0], vsc[1], vw);
+            if (__ballot(mx > m_run + kLazy) != 0) {
+                const float m_new = fmaxf(m_run, mx);
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                m_run = m_new;
+                l_part *= alpha;
+    #pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    ps[g] *= alpha;
+                    o[g][0] *= alpha;
+                    o[g][1] *= alpha;
+                }
+            }
+            float p[2];
+    #pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                p[e] = __builtin_amdgcn_exp2f(t[e] - m_run);
+                l_part += p[e];
+            }
+            float vs[2][G];
+    #pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const half2_t v01 = as_half2(vsc[e][0]), v23 = as_half2(vsc[e][1]);
+                vs[e][0] = (float)v01.x;
+                vs[e][1] = (float)v01.y;
+                vs[e][2] = (float)v23.x;
+                vs[e][3] = (float)v23.y;
+            }
+            // tokens past seq_len: p is 0, and their scale may be anything (NaN included)
+            if (tok0 + kTile > seq_len) {
+    #pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    if (tok0 + T0 + 2 * e >= seq_len) vs[e][0] = vs[e][1] = vs[e][2] = vs[e][3] = 0.0f;
+            }
+            uint32_t pw[G];
+            const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+    #pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const half2_t wp = {(half_t)(p[0] * vs[0][g]), (half_t)(p[1] * vs[1][g])};
+                ps[g] = __builtin_amdgcn_fdot2(wp, one2, ps[g], false);
+                pw[g] = as_u32(wp);
+            }
+            const half8_t pa = __builtin_bit_cast(half8_t, lds_p_transpose(p_wr, pw, p_rd));
+            // group g's 32 dims as byte columns n (even dim lo, odd hi)
+    #pragma unroll
+            for (int g = 0; g < G; ++g) {
+                half8_t lo, hi;
+                v_operands(vw[g], lo, hi);
+                o[g][0] = mfma16x16x32(pa, lo, o[g][0]);
+                o[g][1] = mfma16x16x32(pa, hi, o[g][1]);
+            }
+        };
+
+        // ---- the pipeline.  Step s: wait for this wave's loads of slot s (the
+        // slot s + 1 stays in flight, and s + 2 at step 0); the barrier makes
+        // every wave's slot-s loads visible and frees slot s - 1, which receives
+        // slot s + 2;
+        // the set of parity s runs the first half of tile s, the other set the
+        // second half of tile s - 1.  Every wave passes the n_stages + 1 steps'
+        // barriers; each set has a loop of its own, two steps per iteration, so
+        // that its halves are straight-line code.
+        auto step = [&](int s) __attribute__((always_inline)) -> uint32_t {
+            if (s == 0) wait_vmcnt<kAhead * kJobs>();
+            else wait_vmcnt<(kAhead - 1) * kJobs>();
+            __builtin_amdgcn_s_barrier();
+            if (s > 0) issue(s + kAhead);
+            return lds_addr(smem) + (uint32_t)((s & (kSlots - 1)) * SLOT);
+        };
+        if (par == 0) {
+            int s = 0;
+            for (; s < n_stages; s += 2) {
+                first_half(s, step(s));
+                second_half(s, step(s + 1));
+            }
+            if (s == n_stages) step(s);
+        } else {
+            step(0);
+            int s = 1;
+            for (; s < n_stages; s += 2) {
+                first_half(s, step(s));
+                second_half(s, step(s + 1));
+            }
+            if (s == n_stages) step(s);
+        }
+        wait_vmcnt<0>();  // the empty loads past the chunk still write LDS
+        __syncthreads();
+
+        // ---- each set's (m, l, o) of kv head kvh in LDS area `wave`:
+        // [0, 4) m, [4, 8) l, [8 + h D, ...) o (unnormalised, code offset removed).
+        {
+            l_part = row16_sum(l_part);
+            float psr[G];
+    #pragma unroll
+            for (int g = 0; g < G; ++g) psr[g] = 8.0f * row16_sum(ps[g]);
+            float* const ep = reinterpret_cast<float*>(smem + wave * L::EPI_AREA);
+            if (n == 0) {
+                ep[jq] = m_run;
+                ep[4 + jq] = l_part;
+            }
+    #pragma unroll
+            for (int g = 0; g < G; ++g)
+    #pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    ep[8 + jq * D + 32 * g + 2 * n + e] = o[g][e][g] * (e ? 1048576.0f : 16777216.0f) - psr[g];
+        }
+        __syncthreads();
+
+        // ---- the chunk's result for element idx = (kv head, query head, dim),
+        // 4 dims at a time: the two sets' states combined.  A set without tiles
+        // (a one-tile chunk) has m = -inf, l = 0, o = 0 and weight 0.
+        const int hq = p_n_q_heads;
+        const int total = hq * D, n4 = total / 4;
+        auto chunk4 = [&](int e4, float& m, float& l) -> float4_t {
+            const int idx = 4 * e4;
+            const int j = idx / (GQ * D), rem = idx - j * (GQ * D), h = rem / D, d = rem - h * D;
+            const float* w0 = reinterpret_cast<const float*>(smem + j * L::EPI_AREA);
+            const float* w1 = reinterpret_cast<const float*>(smem + (HKV + j) * L::EPI_AREA);
+            m = fmaxf(w0[h], w1[h]);
+            const float a0 = __builtin_amdgcn_exp2f(w0[h] - m), a1 = __builtin_amdgcn_exp2f(w1[h] - m);
+            l = w0[4 + h] * a0 + w1[4 + h] * a1;
+            const float4_t o0 = *reinterpret_cast<const float4_t*>(w0 + 8 + h * D + d);
+            const float4_t o1 = *reinterpret_cast<const float4_t*>(w1 + 8 + h * D + d);
+            return (o0 * a0 + o1 * a1) * (1.0f / l);
+        };
+        const int64_t out_base = (int64_t)b * total;
+        auto store_out4 = [&](int e4, float4_t v) {
+            if (a.out_f32) {
+                *reinterpret_cast<float4_t*>(reinterpret_cast<float*>(a.out) + out_base + 4 * e4) = v;
+            } else {
+                const half2_t lo = {(half_t)v[0], (half_t)v[1]}, hi = {(half_t)v[2], (half_t)v[3]};
+                *reinterpret_cast<u32x2_t*>(reinterpret_cast<half_t*>(a.out) + out_base + 4 * e4) =
+                    u32x2_t{as_u32(lo), as_u32(hi)};
+            }
+        };
+        if (n_chunks == 1) {
+            for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
+                float m, l;
+                store_out4(e4, chunk4(e4, m, l));
+            }
+            return;
+        }
+
+        if constexpr (!SEG) {
+            // Chunk mode: at most 64 chunks a sequence, merged in one level.
+            // ---- split-KV: publish (o / l, m, l) with device-coherent stores; the
+            // last chunk to arrive merges every chunk of the sequence.
+            const uint32_t part_o = (uint32_t)total * 4, part_ml = (uint32_t)hq * 8;  // bytes per partial
+            const int64_t row0 = (int64_t)b * p_max_chunks;
+            {
+                const auto ro = buf_rsrc(a.part_o + (row0 + chunk) * total, part_o);
+                const auto rm = buf_rsrc(a.part_ml + (row0 + chunk) * hq * 2, part_ml);
+                for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
+                    float m, l;
+                    const float4_t v = chunk4(e4, m, l);
+                    store4_sc1(v, ro, (uint32_t)e4 * 16);
+                    if ((4 * e4) % D == 0) store2_sc1(float2v_t{m, l}, rm, (uint32_t)(4 * e4 / D) * 8);
+                }
+            }
+            wait_vmcnt<0>();
+            __syncthreads();
+            uint32_t* const ctl = reinterpret_cast<uint32_t*>(smem + 2 * HKV * L::EPI_AREA);
+            if (threadIdx.x == 0)
+                ctl[0] = arrive_last(a.counters + (int64_t)b * kCountersPerSeq, (uint32_t)n_chunks) ? 1u : 0u;
+            __syncthreads();
+            if (ctl[0] == 0) return;
+
+            // Merge the M = n_chunks partials, each thread a float4 of the output:
+            // o = sum_c w_c (o / l)_c / sum_c w_c with w_c = l_c 2^(m_c - m*), the
+            // partials and their (m, l) loaded together, kMergeBatch chunks at a
+            // time, m* the running maximum.  This chunk's own partial comes from LDS
+            // (the same values it published).
+            const int M = n_chunks;
+            const auto ro = buf_rsrc(a.part_o + row0 * total, part_o * (uint32_t)M);
+            const auto rm = buf_rsrc(a.part_ml + row0 * hq * 2, part_ml * (uint32_t)M);
+            for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
+                const int h = 4 * e4 / D;
+                float mstar = -INFINITY, lsum = 0.0f;
+                float4_t acc = {0, 0, 0, 0};
+                for (int c0 = 0; c0 < M; c0 += kMergeBatch) {
+                    float4_t oc[kMergeBatch];
+                    float2v_t ml[kMergeBatch];
+        #pragma unroll
+                    for (int cb = 0; cb < kMergeBatch; ++cb) {
+                        const int c = min(c0 + cb, M - 1);
+                        if (c != chunk) {
+                            oc[cb] = load4_sc1(ro, (uint32_t)c * part_o + (uint32_t)e4 * 16);
+                            ml[cb] = load2_sc1(rm, ((uint32_t)c * (uint32_t)hq + (uint32_t)h) * 8);
+                        } else {
+                            float m, l;
+                            oc[cb] = chunk4(e4, m, l);
+                            ml[cb] = float2v_t{m, l};
+                        }
+                    }
+                    // past M: a repeat of partial M - 1 with weight 0
+                    float mb = mstar;
+        #pragma unroll
+                    for (int cb = 0; cb < kMergeBatch; ++cb) mb = fmaxf(mb, ml[cb][0]);
+                    const float r = __builtin_amdgcn_exp2f(mstar - mb);  // 0 on the first batch
+                    acc *= r;
+                    lsum *= r;
+        #pragma unroll
+                    for (int cb = 0; cb < kMergeBatch; ++cb) {
+                        const float w = c0 + cb < M ? ml[cb][1] * __builtin_amdgcn_exp2f(ml[cb][0] - mb) : 0.0f;
+                        acc += oc[cb] * w;
+                        lsum += w;
+                    }
+                    mstar = mb;
+                }
+                store_out4(e4, acc * (1.0f / lsum));
+            }
+        } else {
+            // Balanced mode: up to 8 x 64 chunks a sequence, two levels.
+            // ---- split-KV: publish (o / l, m, l) with device-coherent stores; the
+            // last chunk of each group of kMergeGroup chunks to arrive merges the
+            // group; with more than one group, the group partials go out the same
+            // way and the last group to arrive merges them (two levels, so no
+            // workgroup reads more than kMergeGroup chunk partials or kMaxGroups
+            // group partials).
+            const uint32_t part_o = (uint32_t)total * 4, part_ml = (uint32_t)hq * 8;  // bytes per partial
+            {
+                const auto ro = buf_rsrc(a.part_o + (row0 + chunk) * total, part_o);
+                const auto rm = buf_rsrc(a.part_ml + (row0 + chunk) * hq * 2, part_ml);
+                for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
+                    float m, l;
+                    const float4_t v = chunk4(e4, m, l);
+                    store4_sc1(v, ro, (uint32_t)e4 * 16);
+                    if ((4 * e4) % D == 0) store2_sc1(float2v_t{m, l}, rm, (uint32_t)(4 * e4 / D) * 8);
+                }
+            }
+            wait_vmcnt<0>();
+            __syncthreads();
+            uint32_t* const ctl = reinterpret_cast<uint32_t*>(smem + 2 * HKV * L::EPI_AREA);
+            uint32_t* const seq_ctr = a.counters + (int64_t)b * kCountersPerSeq;
+            // Arrival at a counter (the protocol of arrive_last): true in the
+            // workgroup that completes `expect` arrivals.
+            auto arrive = [&](uint32_t* counter, int expect) __attribute__((always_inline)) -> bool {
+                if (threadIdx.x == 0) ctl[0] = arrive_last(counter, (uint32_t)expect) ? 1u : 0u;
+                __syncthreads();
+                const bool last = ctl[0] != 0;
+                __syncthreads();
+                return last;
+            };
+            // Merge M partials (o / l at po, (m, l) at pm; partial `own` from LDS)
+            // into the output, or into the group partial at (wo, wm): each thread
+            // float4s of it, o = sum_c w_c (o / l)_c / sum_c w_c with
+            // w_c = l_c 2^(m_c - m*), kMergeBatch partials and their (m, l) in
+            // flight, m* the running maximum.
+            auto merge = [&](const float* po, const float* pm, int M, int own, bool to_out, float* wo,
+                             float* wm) __attribute__((always_inline)) {
+                const auto ro = buf_rsrc(po, part_o * (uint32_t)M);
+                const auto rm = buf_rsrc(pm, part_ml * (uint32_t)M);
+                const auto wro = buf_rsrc(wo, to_out ? 0u : part_o);
+                const auto wrm = buf_rsrc(wm, to_out ? 0u : part_ml);
+                for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
+                    const int h = 4 * e4 / D;
+                    float mstar = -INFINITY, lsum = 0.0f;
+                    float4_t acc = {0, 0, 0, 0};
+                    for (int c0 = 0; c0 < M; c0 += kMergeBatch) {
+                        float4_t oc[kMergeBatch];
+                        float2v_t ml[kMergeBatch];
+        #pragma unroll
+                        for (int cb = 0; cb < kMergeBatch; ++cb) {
+                            const int c = min(c0 + cb, M - 1);
+                            if (c != own) {
+                                oc[cb] = load4_sc1(ro, (uint32_t)c * part_o + (uint32_t)e4 * 16);
+                                ml[cb] = load2_sc1(rm, ((uint32_t)c * (uint32_t)hq + (uint32_t)h) * 8);
+                            } else {
+                                float m, l;
+                                oc[cb] = chunk4(e4, m, l);
+                                ml[cb] = float2v_t{m, l};
+                            }
+                        }
+                        // past M: a repeat of partial M - 1 with weight 0
+                        float mb = mstar;
+        #pragma unroll
+                        for (int cb = 0; cb < kMergeBatch; ++cb) mb = fmaxf(mb, ml[cb][0]);
+                        const float r = __builtin_amdgcn_exp2f(mstar - mb);  // 0 on the first batch
+                        acc *= r;
+                        lsum *= r;
+        #pragma unroll
+                        for (int cb = 0; cb < kMergeBatch; ++cb) {
+                            const float w = c0 + cb < M ? ml[cb][1] * __builtin_amdgcn_exp2f(ml[cb][0] - mb) : 0.0f;
+                            acc += oc[cb] * w;
+                            lsum += w;
+                        }
+                        mstar = mb;
+                    }
+                    const float4_t res = acc * (1.0f / lsum);
+                    if (to_out) {
+                        store_out4(e4, res);
+                    } else {
+                        store4_sc1(res, wro, (uint32_t)e4 * 16);
+                        if ((4 * e4) % D == 0) store2_sc1(float2v_t{mstar, lsum}, wrm, (uint32_t)h * 8);
+                    }
+                }
+            };
+            const int grp = chunk / kMergeGroup;
+            const int n_groups = (n_chunks + kMergeGroup - 1) / kMergeGroup;
+            const int members = min(kMergeGroup, n_chunks - grp * kMergeGroup);
+            if (!arrive(seq_ctr + grp, members)) return;
+            const int64_t c0row = row0 + grp * kMergeGroup;
+            merge(a.part_o + c0row * total, a.part_ml + c0row * hq * 2, members, chunk - grp * kMergeGroup, n_groups == 1,
+                  a.grp_o + (row0 + grp) * total, a.grp_ml + (row0 + grp) * hq * 2);
+            if (n_groups == 1) return;
+            wait_vmcnt<0>();
+            __syncthreads();
+            if (!arrive(seq_ctr + kSeqCounter, n_groups)) return;
+            merge(a.grp_o + row0 * total, a.grp_ml + row0 * hq * 2, n_groups, -1, true, a.grp_o, a.grp_ml);
+        }
+    };
+
     if constexpr (!segmented) {
         const int wg = xcd_remap(blockIdx.x, p_nblocks);
-        b = wg / p_max_chunks;
-        chunk = wg % p_max_chunks;
-        t_begin = chunk * p_chunk_tiles;
-        row0 = (int64_t)b * p_max_chunks;
+        const int b = wg / p_max_chunks, chunk = wg % p_max_chunks;
+        run_piece(b, chunk, chunk * p_chunk_tiles, 0, 0, (int64_t)b * p_max_chunks);
     } else {
         const int W = p_max_chunks;
-        const int bid = blockIdx.x;
-        const int w_self = bid < W ? xcd_remap(bid, W) : -1;
-        const int b_self = bid < W ? -1 : bid - W;
-        int* const seg = reinterpret_cast<int*>(smem);            // [6]: the piece found (the ring is still free)
-        long long* const red = reinterpret_cast<long long*>(smem + 64);  // [kWaves]
-        auto tiles_of = [&](int bb) -> long long {
+        const int w_self = xcd_remap(blockIdx.x, W);
+        int* const list = reinterpret_cast<int*>(smem + L::LIST_OFF);    // [kMaxPieces][6], then the count
+        long long* const red = reinterpret_cast<long long*>(smem + 64);  // [kWaves] (the ring is still free)
+        auto units_of = [&](int bb) -> long long {
             const long long t = ((long long)p_seq_lens[bb] + kTile - 1) / kTile;
-            return t > 0 ? t : 0;
+            return t > 0 ? t + kPieceCost : 0;
         };
-        long long part = 0;
-        for (int bb = threadIdx.x; bb < a.batch; bb += 64 * kWaves) part += tiles_of(bb);
-        for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off, 64);
-        if (lane == 0) red[wave] = part;
-        if (threadIdx.x == 0) seg[0] = -1;
+        // Units of this thread's sequence (batches up to the workgroup's 1024
+        // threads) and their inclusive scan over the workgroup: one pass
+        // gives both every sequence's place and the total C.  Larger
+        // batches take a first pass for C and scan in steps of 1024 below.
+        const bool one_pass = a.batch <= 64 * kWaves;
+        long long ub0 = 0, x0 = 0, before0 = 0;
+        long long C = 0;
+        if (one_pass) {
+            ub0 = (int)threadIdx.x < a.batch ? units_of(threadIdx.x) : 0;
+            x0 = ub0;
+            for (int off = 1; off < 64; off <<= 1) {
+                const long long y = __shfl_up(x0, off, 64);
+                if (lane >= off) x0 += y;
+            }
+            if (lane == 63) red[wave] = x0;
+        } else {
+            long long part = 0;
+            for (int bb = threadIdx.x; bb < a.batch; bb += 64 * kWaves) part += units_of(bb);
+            for (int off = 32; off > 0; off >>= 1) part += __shfl_xor(part, off, 64);
+            if (lane == 0) red[wave] = part;
+        }
+        if (threadIdx.x == 0) list[6 * kMaxPieces] = 0;
         __syncthreads();
-        long long T = 0;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) T += red[w];
-        __syncthreads();
-        // At most T ranges, so that none is empty and a sequence's chunks are
-        // numbered without gaps (range workgroups past them have none).
-        const long long Wl = (long long)W < T ? (long long)W : T;
-        if (T > (long long)kMaxChunkTiles * Wl) {
+        for (int w = 0; w < kWaves; ++w) {
+            const long long v = red[w];
+            if (w < wave) before0 += v;
+            C += v;
+        }
+        if (!one_pass) __syncthreads();  // red is reused by the scan below
+        // At most C ranges, so that none is empty and a sequence's chunks are
+        // numbered without gaps.
+        const long long Wl = (long long)W < C ? (long long)W : C;
+        if (C > (long long)kMaxChunkTiles * Wl) {
             // The lengths outgrew the plan (a balanced plan made for fewer
             // tokens): a range would not fit the page-id window.  Every
-            // workgroup sees the same T, so all of them write NaN into the
+            // workgroup sees the same C, so all of them write NaN into the
             // whole output instead of a wrong result.
-            const int64_t n_out = (int64_t)a.batch * p_n_q_heads * D;
+            const int64_t n_out = (int64_t)a.batch * p_n_q_heads * Geo<HKV>::D;
             for (int64_t i = (int64_t)blockIdx.x * (64 * kWaves) + threadIdx.x; i < n_out;
                  i += (int64_t)gridDim.x * (64 * kWaves)) {
                 if (a.out_f32) reinterpret_cast<float*>(a.out)[i] = __builtin_nanf("");
@@ -348,13 +904,31 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
             }
             return;
         }
-        auto range_lo = [&](long long w) -> long long { return w * T / Wl; };
-        auto range_hi = [&](long long w) -> long long { return (w + 1) * T / Wl; };
+        if (w_self >= Wl) return;  // no range (uniform over the workgroup)
+        const long long lo = w_self * C / Wl, hi = (w_self + 1) * C / Wl;
+        auto range_of = [&](long long u) -> long long { return ((u + 1) * Wl - 1) / C; };
+        auto add_piece = [&](int bb, long long ts, long long te) {
+            const long long f = range_of(ts), l = range_of(te - 1);
+            const int k = atomicAdd(&list[6 * kMaxPieces], 1);
+            if (k < kMaxPieces) {
+                list[6 * k + 0] = bb;
+                list[6 * k + 1] = (int)((lo > ts ? lo : ts) - ts);
+                list[6 * k + 2] = (int)((hi < te ? hi : te) - ts);
+                list[6 * k + 3] = (int)(w_self - f);
+                list[6 * k + 4] = (int)(l - f + 1);
+                list[6 * k + 5] = (int)f;
+            }
+        };
+        if (one_pass) {
+            const long long ts = before0 + x0 - ub0 + kPieceCost, te = before0 + x0;  // the tiles' units
+            if (ub0 > 0 && ts < hi && te > lo) add_piece((int)threadIdx.x, ts, te);
+            __syncthreads();
+        }
         long long carry = 0;
-        for (int b0 = 0; b0 < a.batch; b0 += 64 * kWaves) {
+        for (int b0 = 0; !one_pass && b0 < a.batch; b0 += 64 * kWaves) {
             const int bb = b0 + (int)threadIdx.x;
-            const long long nb = bb < a.batch ? tiles_of(bb) : 0;
-            long long x = nb;  // inclusive scan over the wave
+            const long long ub = bb < a.batch ? units_of(bb) : 0;
+            long long x = ub;  // inclusive scan over the wave
             for (int off = 1; off < 64; off <<= 1) {
                 const long long y = __shfl_up(x, off, 64);
                 if (lane >= off) x += y;
@@ -368,557 +942,22 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
                 if (w < wave) before += v;
                 sum += v;
             }
-            const long long pb = carry + before + x - nb;  // the sequence's first tile in the laid-out order
-            if (nb > 0) {
-                long long w = -1;
-                if (w_self >= 0 && w_self < Wl) {
-                    const long long lo = range_lo(w_self);
-                    if (pb <= lo && lo < pb + nb && lo < range_hi(w_self)) w = w_self;
-                } else if (bb == b_self) {
-                    const long long f = ((pb + 1) * Wl - 1) / T;
-                    if (pb > range_lo(f) && pb < range_hi(f)) w = f;
-                }
-                if (w >= 0) {  // at most one thread of the workgroup
-                    const long long f = ((pb + 1) * Wl - 1) / T, l = ((pb + nb) * Wl - 1) / T;
-                    const long long lo = range_lo(w), hi = range_hi(w);
-                    seg[0] = bb;
-                    seg[1] = (int)((lo > pb ? lo : pb) - pb);
-                    seg[2] = (int)((hi < pb + nb ? hi : pb + nb) - pb);
-                    seg[3] = (int)(w - f);
-                    seg[4] = (int)(l - f + 1);
-                    seg[5] = (int)f;
-                }
-            }
+            const long long ts = carry + before + x - ub + kPieceCost, te = carry + before + x;  // the tiles' units
+            if (ub > 0 && ts < hi && te > lo) add_piece(bb, ts, te);
             carry += sum;
             __syncthreads();
         }
-        b = __builtin_amdgcn_readfirstlane(seg[0]);
-        if (b < 0) return;  // no piece (uniform over the workgroup)
-        t_begin = __builtin_amdgcn_readfirstlane(seg[1]);
-        t_lim = __builtin_amdgcn_readfirstlane(seg[2]);
-        chunk = __builtin_amdgcn_readfirstlane(seg[3]);
-        seg_chunks = __builtin_amdgcn_readfirstlane(seg[4]);
-        row0 = (int64_t)__builtin_amdgcn_readfirstlane(seg[5]) + b;
-        __syncthreads();  // the ring's first bytes are loaded into next
-    }
-    const int share = segmented ? -p_chunk_tiles : p_chunk_tiles;
-    const int p0 = 2 * t_begin;
-    const int seq_len = p_seq_lens[b];
-
-    // ---- page ids of the chunk (logical page p0 + i in lane i of pid0 /
-    // pid1) and the raw query rows: neither depends on the sequence length,
-    // so they are in flight together with its load.
-    const int32_t* bt = p_block_table + (int64_t)b * p_bt_cols;
-    // (every lane loads, clamped into the table; no divergent branches
-    // around the loads, so none waits for another)
-    int pid0 = virtual_page(bt, min(p0 + lane, p_max_pages - 1), p_page_shift);
-    int pid1 = virtual_page(bt, min(p0 + 64 + lane, p_max_pages - 1), p_page_shift);
-    // Query A operand: row n = (h, g) = (n >> 2, n & 3), nonzero only where
-    // g == jq: 32 dims of group jq of head h.
-    const half_t* qh = p_q + ((int64_t)b * p_n_q_heads + kvh * GQ) * D;
-    u32x4_t qraw[4];
-    {
-        const half_t* qrow = qh + (n >> 2) * D + 32 * jq;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) qraw[m] = *reinterpret_cast<const u32x4_t*>(qrow + 8 * m);
-    }
-    asm volatile("" ::: "memory");  // keeps the loads above issued before the early return below
-
-    const int n_tiles = (seq_len + kTile - 1) / kTile;
-    if (t_begin >= n_tiles) return;  // uniform over the workgroup
-    const int t_end = segmented ? t_lim : min(t_begin + share, n_tiles);
-    const int n_stages = t_end - t_begin;
-    const int n_chunks = segmented ? seg_chunks : (n_tiles + share - 1) / share;
-    const int last_lp = (seq_len + kPage - 1) / kPage - 1;
-
-    // ---- this wave's three loads of a slot (the same every step); each
-    // fills 1 KiB of the slot, its lanes fetching the page chunks the
-    // swizzles put there:
-    // * K piece `wave` of tile s: page kr, token rows 2 qq and 2 qq + 1;
-    // * V piece `wave` of tile s - 1, the same rows;
-    // * waves 0-3: scales KS p0, KS p1 (tile s), VS p0, VS p1 (tile s - 1);
-    //   waves 4-15: an empty load into the sink.
-    const int kr = wave / PER_PAGE, qq = wave % PER_PAGE;
-    uint32_t k_voff, v_voff, s_voff;
-    {
-        const int P = qq * 64 + lane, row = P / CK, cpos = P % CK;
-        k_voff = (uint32_t)(row * CK + (cpos ^ kkey(row, kr))) * 16;
-        v_voff = (uint32_t)(row * CK + (cpos ^ vswz<CK>(16 * kr + row))) * 16;
-        const int srow = lane >> 2, scol = lane & 3;
-        s_voff = (uint32_t)(srow * 64 + ((scol ^ ((srow >> 2) & 3)) * 16));
-    }
-    const bool s_job = wave < 4;
-    const bool s_is_v = (wave & 2) != 0;
-    const int s_r = wave & 1;
-
-    // Physical page of logical page lp (past the sequence: its last page).
-    auto page_of = [&](int lp) -> int64_t {
-        const int rel = min(lp, last_lp) - p0;
-        return (int64_t)__builtin_amdgcn_readlane(rel < 64 ? pid0 : pid1, rel & 63);
-    };
-    pid0 = (int)opaque((uint32_t)pid0);
-    pid1 = (int)opaque((uint32_t)pid1);
-
-    // Slot of step s: K of tile s, V of tile s - 1.  Halves outside the
-    // chunk load with zero-size descriptors (no memory access; the load still
-    // writes zeros into its LDS bytes), so every wave has kJobs loads of every
-    // slot in flight.
-    auto issue = [&](int s) __attribute__((always_inline)) {
-        uint8_t* const dst = smem + (s & (kSlots - 1)) * SLOT;
-        const bool kv = s < n_stages;
-        const bool vv = s >= 1 && s <= n_stages;
-        const int64_t kp = kv ? page_of(2 * (t_begin + s) + kr) : 0;
-        const int64_t vp = vv ? page_of(2 * (t_begin + s - 1) + kr) : 0;
-        const bool sv = s_job && (s_is_v ? vv : kv);
-        const int64_t sp = sv ? page_of(2 * (t_begin + s - (s_is_v ? 1 : 0)) + s_r) : 0;
-        // (the page sizes are the kernel-scope constants: L::KPAGE named in
-        // these descriptor expressions makes clang drop the kernel's host
-        // launch stub)
-        const auto krs = buf_rsrc(a.k_data + kp * KPAGE, kv ? KPAGE : 0u);
-        const auto vrs = buf_rsrc(a.v_data + vp * KPAGE, vv ? KPAGE : 0u);
-        const auto srs = buf_rsrc((s_is_v ? a.v_scale : a.k_scale) + sp * SPAGE, sv ? SPAGE : 0u);
-        uint8_t* const kdst = dst + L::K_OFF + 1024 * wave;
-        uint8_t* const vdst = dst + L::V_OFF + 1024 * wave;
-        uint8_t* const sdst = s_job ? dst + L::KS_OFF + 1024 * wave : smem + L::SINK_OFF;
-        const uint32_t ko = k_voff, vo = v_voff, so = s_voff;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (IRIS_LDS void*)kdst, 16, ko, 0, 0, kNT);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (IRIS_LDS void*)vdst, 16, vo, 0, 0, kNT);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(srs, (IRIS_LDS void*)sdst, 16, so, 0, 0, kNT);
-    };
-    // The first kAhead + 1 slots stream in while the query operands are
-    // prepared (one slot more than the steady state keeps in flight: the
-    // deeper first queue measured 0.2-0.3 us faster at cfg2, a fourth slot
-    // and a single one slower).
-#pragma unroll
-    for (int s = 0; s <= kAhead; ++s) issue(s);
-
-    half8_t qa[4];
-    {
-        const bool mine = (n & 3) == jq;
-#pragma unroll
-        for (int m = 0; m < 4; ++m) qa[m] = q_operand(mine ? qraw[m] : u32x4_t{0, 0, 0, 0});
-    }
-    // Accumulator start that removes the +8 of the K codes: C row (h, g)
-    // gets -8 * 2^-24 * (sum of q over group g of head h, as the A operand
-    // holds it, high-nibble dims / 16 counted 16 times).  Lane (4 h + g, g)
-    // holds that group in qa; C lane (n, jq) needs rows (jq, 0..3).
-    float4_t init;
-    {
-        float part = 0.0f;
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) part += (float)qa[m][i] * ((i & 2) ? 16.0f : 1.0f);
-        part *= -8.0f * 5.9604644775390625e-08f;
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-            init[g] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
-                                                   4 * (16 * g + 4 * jq + g), __builtin_bit_cast(int, part)));
-    }
-
-    // ---- per-lane LDS offsets within a slot
-    // K operand of chain e: token T = 16 (n >> 3) + 4 ((n & 7) >> 1) + (n & 1) + 2 e,
-    // 16 bytes = dims [32 jq, 32 jq + 32) of head kvh.
-    const int T0 = 16 * (n >> 3) + 4 * ((n & 7) >> 1) + (n & 1);
-    uint32_t k_off[2], ks_off[2], vs_off[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int T = T0 + 2 * e;
-        const int r = T >> 4, row = T & 15;
-        k_off[e] = (uint32_t)(L::K_OFF + r * L::KPAGE + (row * CK + ((kvh * 4 + jq) ^ kkey(row, r))) * 16);
-        const int srow = row * 64 + (((kvh >> 1) ^ ((row >> 2) & 3)) * 16) + (kvh & 1) * 8;
-        ks_off[e] = (uint32_t)(L::KS_OFF + r * L::SPAGE + srow);
-        vs_off[e] = (uint32_t)(L::VS_OFF + r * L::SPAGE + srow);
-    }
-    // Transposed V reads of group g: lane (n, jq) points at token tr_tok's
-    // 8-byte half (n & 1) of group g's chunk; after the 8 x 8 byte transpose
-    // it holds byte column n of 8 tokens (k-slot order of v_operands).
-    uint32_t tr_off[G];
-    {
-        const int trk = n >> 1;
-        const int tr_tok = 4 * jq + (trk & 3) + 16 * (trk >> 2);
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-            tr_off[g] = (uint32_t)(L::V_OFF + (tr_tok >> 4) * L::KPAGE +
-                                   ((tr_tok & 15) * CK + ((kvh * 4 + g) ^ vswz<CK>(tr_tok))) * 16 + 8 * (n & 1));
-    }
-    // P area of the kv head: row (h, g) = 4 h + g, 32 halves in k-slot order
-    // of the tile's token blocks (block jq' = tokens 4 jq' + i of both
-    // pages).  Lane (n, jq) writes tokens T0 and T0 + 2, k-slots
-    // 4 (n >> 3) + 2 (n & 1) and the next, of block (n & 7) >> 1 in rows
-    // (jq, 0..3); it reads row n, block jq (rows (h, g) feed the PV of group
-    // g only: the other groups' rows carry the wrong V scale and their C rows
-    // are discarded).
-    const uint32_t p_base = lds_addr(smem + L::P_OFF + kvh * L::P_AREA);
-    const uint32_t p_wr =
-        p_base + (uint32_t)((jq * 4) * L::P_ROW + (((n & 7) >> 1) * 8 + 4 * (n >> 3) + 2 * (n & 1)) * 2);
-    const uint32_t p_rd = p_base + (uint32_t)(n * L::P_ROW + jq * 16);
-
-    const float c24 = a.log2_scale * 16777216.0f;  // MFMA units -> base-2 logits
-    float m_run = -INFINITY;                       // row maximum, base-2 logits
-    float l_part = 0.0f;
-    float ps[G];  // sums of the PV weights per group (V code offset)
-    float4_t o[G][2];
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-        ps[g] = 0.0f;
-        o[g][0] = o[g][1] = float4_t{0, 0, 0, 0};
-    }
-    float t[2];     // scores (base-2 logits) of tokens T0, T0 + 2: first half -> second half
-    float mx = 0.0f;  // their row maximum
-
-    // First half of tile `stage` (K half of its slot): scores of the lane's
-    // two tokens and the row maximum.  The two QK chains are interleaved.
-    auto first_half = [&](int stage, uint32_t base) __attribute__((always_inline)) {
-        const int tok0 = (t_begin + stage) * kTile;
-        u32x4_t kq[2];
-        u32x2_t ksc[2];
-        lds_tile_reads(base + k_off[0], base + k_off[1], base + ks_off[0], base + ks_off[1], kq[0], kq[1], ksc[0],
-                       ksc[1]);
-        float4_t acc[2] = {init, init};
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-#pragma unroll
-            for (int m = 0; m < 4; ++m) acc[e] = mfma16x16x32(qa[m], k_operand(kq[e][m]), acc[e]);
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const half2_t k01 = as_half2(ksc[e][0]), k23 = as_half2(ksc[e][1]);
-            float s = (float)k01.x * acc[e][0];
-            s = __builtin_fmaf((float)k01.y, acc[e][1], s);
-            s = __builtin_fmaf((float)k23.x, acc[e][2], s);
-            s = __builtin_fmaf((float)k23.y, acc[e][3], s);
-            // base-2 logit; s - s is 0 for a finite score and NaN for +-inf,
-            // so a non-finite K scale or query gives NaN as the eager
-            // dequantisation does, never a -inf that would drop the token
-            t[e] = __builtin_fmaf(s, c24, s - s);
+        const int n_pieces = min(__builtin_amdgcn_readfirstlane(list[6 * kMaxPieces]), kMaxPieces);
+        for (int i = 0; i < n_pieces; ++i) {
+            const int pb = __builtin_amdgcn_readfirstlane(list[6 * i + 0]);
+            const int pt0 = __builtin_amdgcn_readfirstlane(list[6 * i + 1]);
+            const int pt1 = __builtin_amdgcn_readfirstlane(list[6 * i + 2]);
+            const int pc = __builtin_amdgcn_readfirstlane(list[6 * i + 3]);
+            const int pn = __builtin_amdgcn_readfirstlane(list[6 * i + 4]);
+            const int pf = __builtin_amdgcn_readfirstlane(list[6 * i + 5]);
+            __syncthreads();  // every wave is done with the previous piece's LDS
+            run_piece(pb, pc, pt0, pt1, pn, (int64_t)pf + pb);
         }
-        if (tok0 + kTile > seq_len) {
-#pragma unroll
-            for (int e = 0; e < 2; ++e)
-                if (tok0 + T0 + 2 * e >= seq_len) t[e] = -INFINITY;
-        }
-        // row jq = head jq; its maximum is finite (token tok0 < seq_len)
-        mx = row16_max(__builtin_elementwise_maximum(t[0], t[1]));
-    };
-
-    // Second half of tile `stage` (V half of the next slot): online softmax
-    // (lazy rescale), PV weights w = p * v_scale (one fp16 rounding), tokens
-    // T0 and T0 + 2 packed per group, and the PV products.
-    auto second_half = [&](int stage, uint32_t base) __attribute__((always_inline)) {
-        const int tok0 = (t_begin + stage) * kTile;
-        u32x2_t vsc[2];
-        int2v_t vw[G];
-        uint32_t tra[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) tra[g] = base + tr_off[g];
-        lds_v_reads(base + vs_off[0], base + vs_off[1], tra, vsc[0], vsc[1], vw);
-        if (__ballot(mx > m_run + kLazy) != 0) {
-            const float m_new = fmaxf(m_run, mx);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            l_part *= alpha;
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                ps[g] *= alpha;
-                o[g][0] *= alpha;
-                o[g][1] *= alpha;
-            }
-        }
-        float p[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            p[e] = __builtin_amdgcn_exp2f(t[e] - m_run);
-            l_part += p[e];
-        }
-        float vs[2][G];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const half2_t v01 = as_half2(vsc[e][0]), v23 = as_half2(vsc[e][1]);
-            vs[e][0] = (float)v01.x;
-            vs[e][1] = (float)v01.y;
-            vs[e][2] = (float)v23.x;
-            vs[e][3] = (float)v23.y;
-        }
-        // tokens past seq_len: p is 0, and their scale may be anything (NaN included)
-        if (tok0 + kTile > seq_len) {
-#pragma unroll
-            for (int e = 0; e < 2; ++e)
-                if (tok0 + T0 + 2 * e >= seq_len) vs[e][0] = vs[e][1] = vs[e][2] = vs[e][3] = 0.0f;
-        }
-        uint32_t pw[G];
-        const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const half2_t wp = {(half_t)(p[0] * vs[0][g]), (half_t)(p[1] * vs[1][g])};
-            ps[g] = __builtin_amdgcn_fdot2(wp, one2, ps[g], false);
-            pw[g] = as_u32(wp);
-        }
-        const half8_t pa = __builtin_bit_cast(half8_t, lds_p_transpose(p_wr, pw, p_rd));
-        // group g's 32 dims as byte columns n (even dim lo, odd hi)
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            half8_t lo, hi;
-            v_operands(vw[g], lo, hi);
-            o[g][0] = mfma16x16x32(pa, lo, o[g][0]);
-            o[g][1] = mfma16x16x32(pa, hi, o[g][1]);
-        }
-    };
-
-    // ---- the pipeline.  Step s: wait for this wave's loads of slot s (the
-    // slot s + 1 stays in flight, and s + 2 at step 0); the barrier makes
-    // every wave's slot-s loads visible and frees slot s - 1, which receives
-    // slot s + 2;
-    // the set of parity s runs the first half of tile s, the other set the
-    // second half of tile s - 1.  Every wave passes the n_stages + 1 steps'
-    // barriers; each set has a loop of its own, two steps per iteration, so
-    // that its halves are straight-line code.
-    auto step = [&](int s) __attribute__((always_inline)) -> uint32_t {
-        if (s == 0) wait_vmcnt<kAhead * kJobs>();
-        else wait_vmcnt<(kAhead - 1) * kJobs>();
-        __builtin_amdgcn_s_barrier();
-        if (s > 0) issue(s + kAhead);
-        return lds_addr(smem) + (uint32_t)((s & (kSlots - 1)) * SLOT);
-    };
-    if (par == 0) {
-        int s = 0;
-        for (; s < n_stages; s += 2) {
-            first_half(s, step(s));
-            second_half(s, step(s + 1));
-        }
-        if (s == n_stages) step(s);
-    } else {
-        step(0);
-        int s = 1;
-        for (; s < n_stages; s += 2) {
-            first_half(s, step(s));
-            second_half(s, step(s + 1));
-        }
-        if (s == n_stages) step(s);
-    }
-    wait_vmcnt<0>();  // the empty loads past the chunk still write LDS
-    __syncthreads();
-
-    // ---- each set's (m, l, o) of kv head kvh in LDS area `wave`:
-    // [0, 4) m, [4, 8) l, [8 + h D, ...) o (unnormalised, code offset removed).
-    {
-        l_part = row16_sum(l_part);
-        float psr[G];
-#pragma unroll
-        for (int g = 0; g < G; ++g) psr[g] = 8.0f * row16_sum(ps[g]);
-        float* const ep = reinterpret_cast<float*>(smem + wave * L::EPI_AREA);
-        if (n == 0) {
-            ep[jq] = m_run;
-            ep[4 + jq] = l_part;
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int e = 0; e < 2; ++e)
-                ep[8 + jq * D + 32 * g + 2 * n + e] = o[g][e][g] * (e ? 1048576.0f : 16777216.0f) - psr[g];
-    }
-    __syncthreads();
-
-    // ---- the chunk's result for element idx = (kv head, query head, dim),
-    // 4 dims at a time: the two sets' states combined.  A set without tiles
-    // (a one-tile chunk) has m = -inf, l = 0, o = 0 and weight 0.
-    const int hq = p_n_q_heads;
-    const int total = hq * D, n4 = total / 4;
-    auto chunk4 = [&](int e4, float& m, float& l) -> float4_t {
-        const int idx = 4 * e4;
-        const int j = idx / (GQ * D), rem = idx - j * (GQ * D), h = rem / D, d = rem - h * D;
-        const float* w0 = reinterpret_cast<const float*>(smem + j * L::EPI_AREA);
-        const float* w1 = reinterpret_cast<const float*>(smem + (HKV + j) * L::EPI_AREA);
-        m = fmaxf(w0[h], w1[h]);
-        const float a0 = __builtin_amdgcn_exp2f(w0[h] - m), a1 = __builtin_amdgcn_exp2f(w1[h] - m);
-        l = w0[4 + h] * a0 + w1[4 + h] * a1;
-        const float4_t o0 = *reinterpret_cast<const float4_t*>(w0 + 8 + h * D + d);
-        const float4_t o1 = *reinterpret_cast<const float4_t*>(w1 + 8 + h * D + d);
-        return (o0 * a0 + o1 * a1) * (1.0f / l);
-    };
-    const int64_t out_base = (int64_t)b * total;
-    auto store_out4 = [&](int e4, float4_t v) {
-        if (a.out_f32) {
-            *reinterpret_cast<float4_t*>(reinterpret_cast<float*>(a.out) + out_base + 4 * e4) = v;
-        } else {
-            const half2_t lo = {(half_t)v[0], (half_t)v[1]}, hi = {(half_t)v[2], (half_t)v[3]};
-            *reinterpret_cast<u32x2_t*>(reinterpret_cast<half_t*>(a.out) + out_base + 4 * e4) =
-                u32x2_t{as_u32(lo), as_u32(hi)};
-        }
-    };
-    if (n_chunks == 1) {
-        for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
-            float m, l;
-            store_out4(e4, chunk4(e4, m, l));
-        }
-        return;
-    }
-
-    if constexpr (!SEG) {
-        // Chunk mode: at most 64 chunks a sequence, merged in one level.
-        // ---- split-KV: publish (o / l, m, l) with device-coherent stores; the
-        // last chunk to arrive merges every chunk of the sequence.
-        const uint32_t part_o = (uint32_t)total * 4, part_ml = (uint32_t)hq * 8;  // bytes per partial
-        const int64_t row0 = (int64_t)b * p_max_chunks;
-        {
-            const auto ro = buf_rsrc(a.part_o + (row0 + chunk) * total, part_o);
-            const auto rm = buf_rsrc(a.part_ml + (row0 + chunk) * hq * 2, part_ml);
-            for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
-                float m, l;
-                const float4_t v = chunk4(e4, m, l);
-                store4_sc1(v, ro, (uint32_t)e4 * 16);
-                if ((4 * e4) % D == 0) store2_sc1(float2v_t{m, l}, rm, (uint32_t)(4 * e4 / D) * 8);
-            }
-        }
-        wait_vmcnt<0>();
-        __syncthreads();
-        uint32_t* const ctl = reinterpret_cast<uint32_t*>(smem + 2 * HKV * L::EPI_AREA);
-        if (threadIdx.x == 0)
-            ctl[0] = arrive_last(a.counters + (int64_t)b * kCountersPerSeq, (uint32_t)n_chunks) ? 1u : 0u;
-        __syncthreads();
-        if (ctl[0] == 0) return;
-
-        // Merge the M = n_chunks partials, each thread a float4 of the output:
-        // o = sum_c w_c (o / l)_c / sum_c w_c with w_c = l_c 2^(m_c - m*), the
-        // partials and their (m, l) loaded together, kMergeBatch chunks at a
-        // time, m* the running maximum.  This chunk's own partial comes from LDS
-        // (the same values it published).
-        const int M = n_chunks;
-        const auto ro = buf_rsrc(a.part_o + row0 * total, part_o * (uint32_t)M);
-        const auto rm = buf_rsrc(a.part_ml + row0 * hq * 2, part_ml * (uint32_t)M);
-        for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
-            const int h = 4 * e4 / D;
-            float mstar = -INFINITY, lsum = 0.0f;
-            float4_t acc = {0, 0, 0, 0};
-            for (int c0 = 0; c0 < M; c0 += kMergeBatch) {
-                float4_t oc[kMergeBatch];
-                float2v_t ml[kMergeBatch];
-    #pragma unroll
-                for (int cb = 0; cb < kMergeBatch; ++cb) {
-                    const int c = min(c0 + cb, M - 1);
-                    if (c != chunk) {
-                        oc[cb] = load4_sc1(ro, (uint32_t)c * part_o + (uint32_t)e4 * 16);
-                        ml[cb] = load2_sc1(rm, ((uint32_t)c * (uint32_t)hq + (uint32_t)h) * 8);
-                    } else {
-                        float m, l;
-                        oc[cb] = chunk4(e4, m, l);
-                        ml[cb] = float2v_t{m, l};
-                    }
-                }
-                // past M: a repeat of partial M - 1 with weight 0
-                float mb = mstar;
-    #pragma unroll
-                for (int cb = 0; cb < kMergeBatch; ++cb) mb = fmaxf(mb, ml[cb][0]);
-                const float r = __builtin_amdgcn_exp2f(mstar - mb);  // 0 on the first batch
-                acc *= r;
-                lsum *= r;
-    #pragma unroll
-                for (int cb = 0; cb < kMergeBatch; ++cb) {
-                    const float w = c0 + cb < M ? ml[cb][1] * __builtin_amdgcn_exp2f(ml[cb][0] - mb) : 0.0f;
-                    acc += oc[cb] * w;
-                    lsum += w;
-                }
-                mstar = mb;
-            }
-            store_out4(e4, acc * (1.0f / lsum));
-        }
-    } else {
-        // Balanced mode: up to 8 x 64 chunks a sequence, two levels.
-        // ---- split-KV: publish (o / l, m, l) with device-coherent stores; the
-        // last chunk of each group of kMergeGroup chunks to arrive merges the
-        // group; with more than one group, the group partials go out the same
-        // way and the last group to arrive merges them (two levels, so no
-        // workgroup reads more than kMergeGroup chunk partials or kMaxGroups
-        // group partials).
-        const uint32_t part_o = (uint32_t)total * 4, part_ml = (uint32_t)hq * 8;  // bytes per partial
-        {
-            const auto ro = buf_rsrc(a.part_o + (row0 + chunk) * total, part_o);
-            const auto rm = buf_rsrc(a.part_ml + (row0 + chunk) * hq * 2, part_ml);
-            for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
-                float m, l;
-                const float4_t v = chunk4(e4, m, l);
-                store4_sc1(v, ro, (uint32_t)e4 * 16);
-                if ((4 * e4) % D == 0) store2_sc1(float2v_t{m, l}, rm, (uint32_t)(4 * e4 / D) * 8);
-            }
-        }
-        wait_vmcnt<0>();
-        __syncthreads();
-        uint32_t* const ctl = reinterpret_cast<uint32_t*>(smem + 2 * HKV * L::EPI_AREA);
-        uint32_t* const seq_ctr = a.counters + (int64_t)b * kCountersPerSeq;
-        // Arrival at a counter (the protocol of arrive_last): true in the
-        // workgroup that completes `expect` arrivals.
-        auto arrive = [&](uint32_t* counter, int expect) __attribute__((always_inline)) -> bool {
-            if (threadIdx.x == 0) ctl[0] = arrive_last(counter, (uint32_t)expect) ? 1u : 0u;
-            __syncthreads();
-            const bool last = ctl[0] != 0;
-            __syncthreads();
-            return last;
-        };
-        // Merge M partials (o / l at po, (m, l) at pm; partial `own` from LDS)
-        // into the output, or into the group partial at (wo, wm): each thread
-        // float4s of it, o = sum_c w_c (o / l)_c / sum_c w_c with
-        // w_c = l_c 2^(m_c - m*), kMergeBatch partials and their (m, l) in
-        // flight, m* the running maximum.
-        auto merge = [&](const float* po, const float* pm, int M, int own, bool to_out, float* wo,
-                         float* wm) __attribute__((always_inline)) {
-            const auto ro = buf_rsrc(po, part_o * (uint32_t)M);
-            const auto rm = buf_rsrc(pm, part_ml * (uint32_t)M);
-            const auto wro = buf_rsrc(wo, to_out ? 0u : part_o);
-            const auto wrm = buf_rsrc(wm, to_out ? 0u : part_ml);
-            for (int e4 = threadIdx.x; e4 < n4; e4 += blockDim.x) {
-                const int h = 4 * e4 / D;
-                float mstar = -INFINITY, lsum = 0.0f;
-                float4_t acc = {0, 0, 0, 0};
-                for (int c0 = 0; c0 < M; c0 += kMergeBatch) {
-                    float4_t oc[kMergeBatch];
-                    float2v_t ml[kMergeBatch];
-    #pragma unroll
-                    for (int cb = 0; cb < kMergeBatch; ++cb) {
-                        const int c = min(c0 + cb, M - 1);
-                        if (c != own) {
-                            oc[cb] = load4_sc1(ro, (uint32_t)c * part_o + (uint32_t)e4 * 16);
-                            ml[cb] = load2_sc1(rm, ((uint32_t)c * (uint32_t)hq + (uint32_t)h) * 8);
-                        } else {
-                            float m, l;
-                            oc[cb] = chunk4(e4, m, l);
-                            ml[cb] = float2v_t{m, l};
-                        }
-                    }
-                    // past M: a repeat of partial M - 1 with weight 0
-                    float mb = mstar;
-    #pragma unroll
-                    for (int cb = 0; cb < kMergeBatch; ++cb) mb = fmaxf(mb, ml[cb][0]);
-                    const float r = __builtin_amdgcn_exp2f(mstar - mb);  // 0 on the first batch
-                    acc *= r;
-                    lsum *= r;
-    #pragma unroll
-                    for (int cb = 0; cb < kMergeBatch; ++cb) {
-                        const float w = c0 + cb < M ? ml[cb][1] * __builtin_amdgcn_exp2f(ml[cb][0] - mb) : 0.0f;
-                        acc += oc[cb] * w;
-                        lsum += w;
-                    }
-                    mstar = mb;
-                }
-                const float4_t res = acc * (1.0f / lsum);
-                if (to_out) {
-                    store_out4(e4, res);
-                } else {
-                    store4_sc1(res, wro, (uint32_t)e4 * 16);
-                    if ((4 * e4) % D == 0) store2_sc1(float2v_t{mstar, lsum}, wrm, (uint32_t)h * 8);
-                }
-            }
-        };
-        const int grp = chunk / kMergeGroup;
-        const int n_groups = (n_chunks + kMergeGroup - 1) / kMergeGroup;
-        const int members = min(kMergeGroup, n_chunks - grp * kMergeGroup);
-        if (!arrive(seq_ctr + grp, members)) return;
-        const int64_t c0row = row0 + grp * kMergeGroup;
-        merge(a.part_o + c0row * total, a.part_ml + c0row * hq * 2, members, chunk - grp * kMergeGroup, n_groups == 1,
-              a.grp_o + (row0 + grp) * total, a.grp_ml + (row0 + grp) * hq * 2);
-        if (n_groups == 1) return;
-        wait_vmcnt<0>();
-        __syncthreads();
-        if (!arrive(seq_ctr + kSeqCounter, n_groups)) return;
-        merge(a.grp_o + row0 * total, a.grp_ml + row0 * hq * 2, n_groups, -1, true, a.grp_o, a.grp_ml);
     }
 }
 
@@ -975,6 +1014,25 @@ static StreamWorkspace stream_workspace(int64_t batch, int64_t num_q_heads, int6
     return w;
 }
 
+int stream_balanced_plan(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t total_tokens,
+                         int32_t* out_chunk_tiles, int32_t* out_max_chunks, int64_t* out_workspace_bytes) {
+    // Units: every sequence's tiles plus kPieceCost (at most units_ub of
+    // them for these lengths); one range a CU (256), each within the page-id
+    // window and at least one piece's start cost plus a tile long.
+    const int64_t units_ub = (total_tokens + st::kTile - 1) / st::kTile + batch * (1 + st::kPieceCost);
+    int64_t per_wg = (units_ub + 255) / 256;
+    if (per_wg < st::kPieceCost + 1) per_wg = st::kPieceCost + 1;
+    if (per_wg > st::kMaxChunkTiles) per_wg = st::kMaxChunkTiles;
+    const int64_t wgs = (units_ub + per_wg - 1) / per_wg;
+    if (wgs > st::kMergeGroup * st::kMaxGroups) return kInvalidArgument;
+    const int64_t share = (units_ub + wgs - 1) / wgs;
+    *out_chunk_tiles = -(int32_t)share;  // negative: the balanced mode
+    *out_max_chunks = (int32_t)wgs;
+    *out_workspace_bytes =
+        wgs > 1 ? stream_workspace(batch, num_q_heads, head_dim, wgs + batch, wgs > st::kMergeGroup).total : 0;
+    return kOk;
+}
+
 int64_t stream_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t max_chunks) {
     return stream_workspace(batch, num_q_heads, head_dim, batch * max_chunks, false).total;  // chunk mode: one level
 }
@@ -986,14 +1044,14 @@ int stream_launch(const void* query, const void* k_data, const void* v_data, con
                   float softmax_scale, int32_t chunk_tiles, int32_t max_chunks, void* stream) {
     if (!stream_supported(num_q_heads, num_kv_heads, head_dim)) return kInvalidArgument;
     // chunk_tiles > 0: chunk mode, batch x max_chunks workgroups; < 0: the
-    // balanced mode, max_chunks ranges of at most -chunk_tiles tiles plus
-    // one sequence-start workgroup per sequence.
+    // balanced mode, max_chunks ranges of at most -chunk_tiles units, a
+    // workgroup each (stream_balanced_plan).
     const bool balanced = chunk_tiles < 0;
     const int64_t share = balanced ? -(int64_t)chunk_tiles : chunk_tiles;
     if (share <= 0 || share > st::kMaxChunkTiles || max_chunks <= 0) return kInvalidArgument;
     if (balanced ? max_chunks > st::kMergeGroup * st::kMaxGroups : max_chunks > st::kMaxChunks) return kInvalidArgument;
     if (!balanced && share * max_chunks * 2 < max_pages) return kInvalidArgument;  // the grid covers every page
-    const int64_t nblocks = balanced ? max_chunks + batch : batch * (int64_t)max_chunks;
+    const int64_t nblocks = balanced ? max_chunks : batch * (int64_t)max_chunks;
     if (nblocks > 0x7FFFFFFF) return kInvalidArgument;
     st::Args a;
     a.q = (const half_t*)query;
