@@ -81,6 +81,13 @@ __device__ __forceinline__ float row16_sum(float x) {
 // scale over nonzero codes whose products all have one sign, where eager
 // gives a finite result for a -inf logit and the kernels NaN.)
 constexpr float kNonFinite = __builtin_nanf("");
+// x through an empty asm: the compiler cannot see where the value comes
+// from, so code using it stays where it is written (masking compares of a
+// sequence's last tile are not hoisted out of their branch into every tile).
+__device__ __forceinline__ int opaque_int(int x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
 __device__ __forceinline__ float poison_if_neg_inf(float lowest, float l) {
     return lowest == -INFINITY ? kNonFinite : l;
 }

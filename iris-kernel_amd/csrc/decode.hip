@@ -812,21 +812,22 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
         // canonicalised operands after the masking selects; the scores are
         // finite or -inf.)
         const int nval = seq_len - tok_base - 4 * jq;
-        float lo;  // lowest score of the valid tokens (-inf: a non-finite K scale or query)
+        // lowest score of the valid tokens (-inf: a non-finite K scale or
+        // query); v_minimum3 needs no canonicalised operands
+        auto vmin = [](float x, float y) { return __builtin_elementwise_minimum(x, y); };
         if (full) {
-            lo = fminf(fminf(fminf(s[0][0], s[0][1]), fminf(s[0][2], s[0][3])),
-                       fminf(fminf(s[1][0], s[1][1]), fminf(s[1][2], s[1][3])));
+            s_lo = vmin(vmin(s_lo, vmin(vmin(s[0][0], s[0][1]), vmin(s[0][2], s[0][3]))),
+                        vmin(vmin(s[1][0], s[1][1]), vmin(s[1][2], s[1][3])));
         } else {
-            lo = INFINITY;
+            const int nv = opaque_int(nval);  // (the compares stay in this branch)
 #pragma unroll
             for (int r = 0; r < 2; ++r)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    if (16 * r + i >= nval) s[r][i] = -INFINITY;
-                    else lo = fminf(lo, s[r][i]);
+                    if (16 * r + i >= nv) s[r][i] = -INFINITY;
+                    else s_lo = vmin(s_lo, s[r][i]);
                 }
         }
-        s_lo = fminf(s_lo, lo);
         auto vmax = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
         float mx = vmax(vmax(vmax(s[0][0], s[0][1]), vmax(s[0][2], s[0][3])),
                         vmax(vmax(s[1][0], s[1][1]), vmax(s[1][2], s[1][3])));
@@ -1009,7 +1010,8 @@ __device__ __forceinline__ void decode_body(const DecodeArgs& a) {
             const bool v0 = full || tok_base + n < seq_len, v1 = full || tok_base + 16 + n < seq_len;
 #pragma unroll
             for (int w = 0; w < 4; ++w)
-                vlo[w] = fminf(vlo[w], fminf(v0 ? sc[0][w] : INFINITY, v1 ? sc[1][w] : INFINITY));
+                vlo[w] = __builtin_elementwise_minimum(
+                    vlo[w], __builtin_elementwise_minimum(v0 ? sc[0][w] : INFINITY, v1 ? sc[1][w] : INFINITY));
         }
         if (!full) {
 #pragma unroll

@@ -363,21 +363,25 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
             }
         }
         const int nval = seq_len - tok0 - 4 * jq;
-        float lo;  // lowest score of the valid tokens (-inf: a non-finite K scale or query)
+        // lowest score of the valid tokens (-inf: a non-finite K scale or
+        // query); v_minimum3 (NaN-propagating: a NaN score poisons the head
+        // through p anyway) needs no canonicalised operands
+        auto vmin = [](float x, float y) { return __builtin_elementwise_minimum(x, y); };
         if (full) {
-            lo = fminf(fminf(fminf(s[0][0], s[0][1]), fminf(s[0][2], s[0][3])),
-                       fminf(fminf(s[1][0], s[1][1]), fminf(s[1][2], s[1][3])));
+            s_lo = vmin(vmin(s_lo, vmin(vmin(s[0][0], s[0][1]), vmin(s[0][2], s[0][3]))),
+                        vmin(vmin(s[1][0], s[1][1]), vmin(s[1][2], s[1][3])));
         } else {
-            lo = INFINITY;
+            // (the count through an opaque copy made here: the compares below
+            // cannot be hoisted out of this branch into every tile)
+            const int nv = opaque_int(nval);
 #pragma unroll
             for (int e = 0; e < 2; ++e)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    if (16 * e + i >= nval) s[e][i] = -INFINITY;
-                    else lo = fminf(lo, s[e][i]);
+                    if (16 * e + i >= nv) s[e][i] = -INFINITY;
+                    else s_lo = vmin(s_lo, s[e][i]);
                 }
         }
-        s_lo = fminf(s_lo, lo);
         auto vmax = [](float x, float y) { return __builtin_elementwise_maximum(x, y); };
         float mx = vmax(vmax(vmax(s[0][0], s[0][1]), vmax(s[0][2], s[0][3])),
                         vmax(vmax(s[1][0], s[1][1]), vmax(s[1][2], s[1][3])));
@@ -411,12 +415,12 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
         if (!full) {
             // Tokens past seq_len may hold any bytes: never let their scale
             // reach the product (0 * NaN).  A real branch.
-            asm volatile("");
+            const int nv = opaque_int(nval);
 #pragma unroll
             for (int e = 0; e < 2; ++e)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    if (16 * e + i >= nval) vsd[e][i] = 0u;
+                    if (16 * e + i >= nv) vsd[e][i] = 0u;
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) {

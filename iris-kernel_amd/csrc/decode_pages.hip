@@ -584,21 +584,22 @@ __global__ __launch_bounds__(64 * kMaxWaves) void int4_decode_pages_kernel(Args 
 #pragma unroll
             for (int i = 0; i < 4; ++i) s[r][i] = group_sum<GS>(s[r][i]);
         // ---- online softmax (base 2, lazy rescale)
-        float lo;  // lowest score of the valid tokens (-inf: a non-finite K scale or query)
+        // lowest score of the valid tokens (-inf: a non-finite K scale or
+        // query); v_minimum3 needs no canonicalised operands
+        auto vmin = [](float x, float y) { return __builtin_elementwise_minimum(x, y); };
         if (full) {
-            lo = fminf(fminf(fminf(s[0][0], s[0][1]), fminf(s[0][2], s[0][3])),
-                       fminf(fminf(s[1][0], s[1][1]), fminf(s[1][2], s[1][3])));
+            s_lo = vmin(vmin(s_lo, vmin(vmin(s[0][0], s[0][1]), vmin(s[0][2], s[0][3]))),
+                        vmin(vmin(s[1][0], s[1][1]), vmin(s[1][2], s[1][3])));
         } else {
-            lo = INFINITY;
+            const int sl = opaque_int(seq_len);  // (the compares stay in this branch)
 #pragma unroll
             for (int r = 0; r < 2; ++r)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    if (tok0 + 16 * r + 4 * jq + i >= seq_len) s[r][i] = -INFINITY;
-                    else lo = fminf(lo, s[r][i]);
+                    if (tok0 + 16 * r + 4 * jq + i >= sl) s[r][i] = -INFINITY;
+                    else s_lo = vmin(s_lo, s[r][i]);
                 }
         }
-        s_lo = fminf(s_lo, lo);
         float mx = fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])),
                          fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
         mx = row_max4(mx);  // finite: token tok0 < seq_len
