@@ -73,18 +73,19 @@ def append_bytes(n_tok, n_kv, d, n_pos) -> int:
 
 def decode_kernel_name(plan, group: int, n_kv: int, d: int, batch: int, max_pages: int) -> str:
     """Name of the decode kernel a plan runs, as rocprofv3 reports it.  16-wave
-    plans: the streaming kernel for its shape (D=128, Hkv=8, 4 query heads per
-    kv head) in chunk mode with at most 64 chunks or in balanced mode (a
-    negative chunk_tiles) with at most 512 ranges, the MQA streaming kernel for
-    one kv head at D=64, else the page-streaming kernel (always, with the
-    page-kernel bit in the plan's wave count); other plans: the general kernel
-    (its VALU-tile variant with the VALU bit)."""
+    plans: the streaming kernel for its shapes (D=128, Hkv=8, 4 or 8 query
+    heads per kv head) in chunk mode with at most 64 chunks or, at 4, in
+    balanced mode (a negative chunk_tiles) with at most 512 ranges, the MQA
+    streaming kernel for one kv head at D=64, else the page-streaming kernel
+    (always, with the page-kernel bit in the plan's wave count); other plans:
+    the general kernel (its VALU-tile variant with the VALU bit)."""
     waves, page_bit, valu_bit = plan[2] & 0xFF, plan[2] & 0x100, plan[2] & 0x200
     balanced = plan[0] < 0
-    if (waves == 16 and not page_bit and d == 128 and n_kv == 8 and group == 4
+    if (waves == 16 and not page_bit and d == 128 and n_kv == 8 and (group == 4 or (group == 8 and not balanced))
             and plan[1] <= (512 if balanced else 64)):
         # (rocprofv3 prints this kernel mangled: _Float16 in its signature)
-        return f"_ZN4iris2st25int4_decode_stream_kernelILi8ELb{int(balanced)}EEEvPKiS3_PKDF16_iiiiiiiNS0_4ArgsE"
+        return (f"_ZN4iris2st25int4_decode_stream_kernelILi8ELi{group}ELb{int(balanced)}EEEvPKiS3_PKDF16_"
+                "iiiiiiiNS0_4ArgsE")
     if waves == 16 and not page_bit and n_kv == 1 and d == 64 and group <= 16:
         return "_ZN4iris2mq22int4_decode_mqa_kernelEPKiS2_PKDF16_iiiiiiNS0_4ArgsE"  # (printed mangled)
     if waves == 16:

@@ -67,6 +67,7 @@
 #include "decode_any.h"
 #include "decode_mqa.h"
 #include "decode_pages.h"
+#include "decode_stream.h"
 #include "iris_hip.h"
 
 namespace iris {
@@ -1396,7 +1397,17 @@ static bool pages_allowed(int32_t waves_per_block) {
     return (selection_of(waves_per_block) & (kValuTile | kAnyKernel)) == 0 && (w == 0 || w == pages_waves());
 }
 static bool pages_preferred(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-                            int64_t total_tokens, int64_t max_tokens, bool lengths_known) {
+                            int64_t max_pages, int64_t total_tokens, int64_t max_tokens, bool lengths_known,
+                            bool page_kernel) {
+    // 8 query heads per kv head: only the streaming kernel's chunk mode (its
+    // chunks cover at most stream_max_chunks() x 64 tiles of the block table),
+    // for batches of similar lengths (configuration 5: B=4, L=131072); the
+    // page kernel's g=8 layout is slower there than the general kernel.
+    if (num_q_heads == 8 * num_kv_heads && stream_supported(num_q_heads, num_kv_heads, head_dim)) {
+        if (page_kernel || max_pages * kPageSize > (int64_t)stream_max_chunks() * 64 * kTile) return false;
+        if (total_tokens * num_kv_heads * (head_dim + head_dim / 8) < kPagesMinBytes) return false;
+        return 4 * total_tokens >= 3 * batch * max_tokens;
+    }
     if (head_dim != 128 || num_kv_heads < 4 || num_q_heads > 4 * num_kv_heads) return false;
     // Below ~100 MB of K/V the launch is too short for the page kernel's
     // deep pipeline (one workgroup per CU, a few stages each) and the
@@ -1455,8 +1466,8 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
         return kOk;
     if (pages_allowed(waves_per_block) && pages_supported(num_q_heads, num_kv_heads, head_dim, max_pages) &&
         (waves_of(waves_per_block) == pages_waves() ||
-         pages_preferred(batch, num_q_heads, num_kv_heads, head_dim, est_total, est_max,
-                         total_tokens >= 0 && max_tokens >= 0))) {
+         pages_preferred(batch, num_q_heads, num_kv_heads, head_dim, max_pages, est_total, est_max,
+                         total_tokens >= 0 && max_tokens >= 0, (sel & kPageKernel) != 0))) {
         const int st = pages_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, total_tokens, max_tokens,
                                   tokens_per_split, (sel & kPageKernel) == 0, out_chunk_tiles, out_max_chunks,
                                   out_waves, out_workspace_bytes);

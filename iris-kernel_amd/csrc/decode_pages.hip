@@ -1101,10 +1101,14 @@ int pages_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t
     if (total_tokens < 0) total_tokens = batch * max_tokens;
     const int64_t max_tiles = (cap_tokens + pg::kTile - 1) / pg::kTile;
     const int64_t longest_tiles = (max_tokens + pg::kTile - 1) / pg::kTile;
-    if (known && tokens_per_split <= 0 && total_tokens < batch * max_tokens) {
+    // The streaming kernel's chunk mode at 8 query heads per kv head (it has
+    // no balanced mode there): chunk plans only.
+    const bool stream_chunks_only = allow_stream && stream_supported(num_q_heads, num_kv_heads, head_dim) &&
+                                    !stream_balanced_supported(num_q_heads, num_kv_heads, head_dim);
+    if (known && tokens_per_split <= 0 && total_tokens < batch * max_tokens && !stream_chunks_only) {
         // The streaming kernel's shape runs its own balanced mode (one range
         // a CU, a workgroup walking every piece of its range).
-        if (allow_stream && stream_supported(num_q_heads, num_kv_heads, head_dim) &&
+        if (allow_stream && stream_balanced_supported(num_q_heads, num_kv_heads, head_dim) &&
             stream_balanced_plan(batch, num_q_heads, head_dim, total_tokens, out_chunk_tiles, out_max_chunks,
                                  out_workspace_bytes) == kOk) {
             *out_waves = kWaves;
@@ -1150,6 +1154,12 @@ int pages_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t
         chunk_tiles = (chunk_tiles + geo.ts - 1) / geo.ts * geo.ts;
     }
     if (chunk_tiles < 1) chunk_tiles = 1;
+    // The streaming kernel's chunks at 8 query heads per kv head: at most
+    // stream_max_chunks() a sequence.
+    if (stream_chunks_only) {
+        const int64_t min_tiles = (max_tiles + stream_max_chunks() - 1) / stream_max_chunks();
+        if (chunk_tiles < min_tiles) chunk_tiles = min_tiles;
+    }
     if (chunk_tiles > pg::kMaxChunkTiles) chunk_tiles = pg::kMaxChunkTiles;
     // One chunk per sequence when the longest one fits in a chunk.
     if (chunk_tiles >= longest_tiles && max_tiles <= pg::kMaxChunkTiles) chunk_tiles = max_tiles;
@@ -1162,7 +1172,13 @@ int pages_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t
     *out_chunk_tiles = (int32_t)chunk_tiles;
     *out_max_chunks = (int32_t)max_chunks;
     *out_waves = kWaves;
-    *out_workspace_bytes = max_chunks > 1 ? pages_workspace_bytes(batch, num_q_heads, head_dim, max_chunks) : 0;
+    int64_t ws = max_chunks > 1 ? pages_workspace_bytes(batch, num_q_heads, head_dim, max_chunks) : 0;
+    if (max_chunks > 1 && allow_stream && stream_supported(num_q_heads, num_kv_heads, head_dim) &&
+        max_chunks <= stream_max_chunks()) {
+        const int64_t sw = stream_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, max_chunks);
+        if (sw > ws) ws = sw;
+    }
+    *out_workspace_bytes = ws;
     return kOk;
 }
 
@@ -1188,8 +1204,9 @@ int pages_launch(const void* query, const void* k_data, const void* v_data, cons
     // The shapes the streaming kernel has (decode_stream.hip), in either
     // mode: it runs them instead (allow_stream false keeps this kernel, for
     // A/B measurements).  Its workspace layout is this kernel's.
-    if (allow_stream && stream_supported(num_q_heads, num_kv_heads, head_dim) &&
-        (balanced ? max_chunks <= 8 * pg::kMaxGroups : max_chunks <= stream_max_chunks()))
+    if (allow_stream &&
+        (balanced ? stream_balanced_supported(num_q_heads, num_kv_heads, head_dim) && max_chunks <= 8 * pg::kMaxGroups
+                  : stream_supported(num_q_heads, num_kv_heads, head_dim) && max_chunks <= stream_max_chunks()))
         return stream_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
                              workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, max_pages,
                              bt_cols, page_shift, softmax_scale, chunk_tiles, max_chunks, stream);

@@ -9,8 +9,11 @@
 
 namespace iris {
 
-// head_dim 128, 8 kv heads, 4 query heads per kv head.
+// head_dim 128, 8 kv heads, 4 or 8 query heads per kv head (chunk mode).
 IRIS_INTERNAL bool stream_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim);
+
+// The shapes of the balanced mode: head_dim 128, 8 kv heads, 4 query heads per kv head.
+IRIS_INTERNAL bool stream_balanced_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim);
 
 // Most chunks per sequence a launch can merge.
 IRIS_INTERNAL int stream_max_chunks();
@@ -22,9 +25,9 @@ IRIS_INTERNAL int stream_balanced_plan(int64_t batch, int64_t num_q_heads, int64
                                        int32_t* out_chunk_tiles, int32_t* out_max_chunks,
                                        int64_t* out_workspace_bytes);
 
-// Split-KV workspace of a launch with max_chunks chunks per sequence.
-IRIS_INTERNAL int64_t stream_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim,
-                                             int64_t max_chunks);
+// Split-KV workspace of a chunk-mode launch with max_chunks chunks per sequence.
+IRIS_INTERNAL int64_t stream_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                                             int64_t head_dim, int64_t max_chunks);
 
 // Chunk-mode launch: batch x max_chunks workgroups of chunk_tiles 32-token tiles.
 IRIS_INTERNAL int stream_launch(const void* query, const void* k_data, const void* v_data, const void* k_scale,

@@ -2,8 +2,9 @@
 //
 // Replaces the TileLang kernel `_int4_paged_decode_attention`
 // (src/iris_kernel/fused_attention.py:11-220 in Hunter2030ZeRo/Iris-Kernel)
-// for head_dim 128, 4 query heads per kv head and 8 kv heads (the GQA shape
-// of Llama-3-8B and its relatives); it computes the result of
+// for head_dim 128, 8 kv heads and 4 or 8 query heads per kv head (the GQA
+// shapes of Llama-3-8B and of Llama-3-70B and its relatives); it computes
+// the result of
 // `torch_eager_int4_paged_decode_attention`
 // (src/iris_kernel/torch_eager_attention.py:154-239).
 //
@@ -52,6 +53,24 @@
 //   kept, the others discarded.
 // * The two sets' softmax states of a kv head are combined in the epilogue.
 //
+// 8 query heads per kv head (GQ 8): the same MFMA counts per tile, the rows
+// pairing heads with groups two at a time.
+// * QK: A row (h, e) = head h (8), e in {0, 1}; MFMA (P, m) covers groups
+//   2 P and 2 P + 1, k-chunks jq = 0, 1 of group 2 P and 2, 3 of group
+//   2 P + 1 (16 dims of each group an MFMA, two MFMAs a pair), A row (h, e)
+//   zero unless e == jq >> 1.  Accumulator P's C lane (token column n, jq)
+//   holds groups 2 P, 2 P + 1 of heads 2 jq and 2 jq + 1: each score is still
+//   4 FMAs, two heads a lane.
+// * PV: A row (h, e) = p[h, t] * v_scale[t, 2 P + e] for group pair P (two
+//   A operands a tile, through the P area one after the other); the
+//   transposed V reads take 8 bytes of group 2 P and 8 of group 2 P + 1, so
+//   B column n is a byte column of group 2 P + (n >> 3) and half of each
+//   MFMA's C rows are kept (a quarter at GQ 4).
+// * Loop: 268 VALU and 16 MFMA per two steps a wave against 209 and 16 at
+//   GQ 4, for twice the query heads.
+// * Chunk mode only; its partials (32 KiB a chunk at 64 query heads) merge in
+//   two levels, groups of 8 chunks.
+//
 // Split-KV: sequences longer than one chunk publish (m, l, o / l) per query
 // head; the last chunk to arrive merges them in the same launch.
 #include "common.h"
@@ -76,6 +95,11 @@ constexpr int kMergeBatch = 8;      // partials in flight per thread in the merg
 // the faster up to about 32 partials (configuration 3: up to 20 a sequence).
 constexpr int kMergeGroup = 32;
 constexpr int kMaxGroups = 64;      // groups merged by the last group
+// Chunk mode at 8 query heads per kv head: a chunk's partial is 32 KiB at 64
+// query heads (twice the GQ 4 one), and up to 64 chunks a sequence would put
+// 2 MiB through the one merging CU; groups of 8 (7 partials read by each
+// group's last arrival, then at most 8 group partials by the last group).
+constexpr int kMergeGroup8 = 8;
 constexpr int kSeqCounter = kCountersPerSeq - 1;  // a sequence's group-level arrival counter
 // Balanced mode: what starting a piece costs, in 32-token tiles of
 // streaming (the epilogue, publish and arrival of the piece before, the
@@ -96,11 +120,12 @@ typedef int int2v_t __attribute__((ext_vector_type(2)));
 typedef float float2v_t __attribute__((ext_vector_type(2)));
 #define IRIS_LDS __attribute__((address_space(3)))
 
-// Geometry of the supported shape: head_dim 128 (4 scale groups), 4 query
-// heads per kv head, HKV kv heads.
-template <int HKV>
+// Geometry of the supported shapes: head_dim 128 (4 scale groups), GQ (4 or
+// 8) query heads per kv head, HKV kv heads.
+template <int HKV, int GQ_>
 struct Geo {
-    static constexpr int D = 128, G = 4, GQ = 4;
+    static constexpr int D = 128, G = 4, GQ = GQ_;
+    static constexpr int NH = GQ / 4;  // query heads of a lane (the C row quad jq holds heads NH jq ..)
     static constexpr int CK = HKV * 4;           // 16-byte chunks per token row of K or V data
     static constexpr int KPAGE = 16 * HKV * 64;  // data bytes of a page (per tensor)
     static constexpr int SPAGE = 16 * HKV * 8;   // scale bytes of a page (per tensor)
@@ -115,7 +140,7 @@ struct Geo {
     static constexpr int P_ROW = 80, P_AREA = 16 * P_ROW, P_OFF = kSlots * SLOT;
     // The empty scale-load slot of waves 4-15 writes (zeros) here.
     static constexpr int SINK_OFF = P_OFF + HKV * P_AREA;
-    static constexpr int EPI_AREA = (8 + GQ * D) * 4;  // one set's (m, l, o) of a kv head in the epilogue
+    static constexpr int EPI_AREA = (2 * GQ + GQ * D) * 4;  // one set's (m, l, o) of a kv head in the epilogue
     // The balanced mode's piece list (the ring, P areas and sink stay clear of it).
     static constexpr int LIST_OFF = SINK_OFF + 1024;
     static constexpr int LDS_MAIN = LIST_OFF + (6 * kMaxPieces + 4) * 4;
@@ -225,6 +250,21 @@ __device__ __forceinline__ void lds_tile_reads(uint32_t k0, uint32_t k1, uint32_
         : "v"(k0), "v"(k1), "v"(ks0), "v"(ks1)
         : "memory");
 }
+// GQ 8: each chain's K operands are two 8-byte pieces (group pairs 0 and 1).
+__device__ __forceinline__ void lds_tile_reads8(uint32_t k00, uint32_t k01, uint32_t k10, uint32_t k11, uint32_t ks0,
+                                                uint32_t ks1, u32x2_t (&kq)[2][2], u32x2_t& ksc0, u32x2_t& ksc1) {
+    asm volatile(
+        "ds_read_b64 %0, %6\n\t"
+        "ds_read_b64 %1, %7\n\t"
+        "ds_read_b64 %2, %8\n\t"
+        "ds_read_b64 %3, %9\n\t"
+        "ds_read_b64 %4, %10\n\t"
+        "ds_read_b64 %5, %11\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(kq[0][0]), "=&v"(kq[0][1]), "=&v"(kq[1][0]), "=&v"(kq[1][1]), "=&v"(ksc0), "=&v"(ksc1)
+        : "v"(k00), "v"(k01), "v"(k10), "v"(k11), "v"(ks0), "v"(ks1)
+        : "memory");
+}
 __device__ __forceinline__ void lds_v_reads(uint32_t vs0, uint32_t vs1, const uint32_t (&tr)[4], u32x2_t& vsc0,
                                             u32x2_t& vsc1, int2v_t (&w)[4]) {
     asm volatile(
@@ -258,6 +298,32 @@ __device__ __forceinline__ u32x4_t lds_p_transpose(uint32_t wr, const uint32_t (
     return a;
 }
 
+// GQ 8: both group pairs' A operands through the same P area, with no wait
+// between the LDS operations: one wave's LDS instructions execute in program
+// order, so each read sees the writes before it and the second pair's writes
+// do not overtake the first pair's read.  (The same sequence with a wait
+// after each step gave bit-identical results and took 7% longer at
+// configuration 5.)
+__device__ __forceinline__ void lds_p_transpose2(uint32_t wr, const uint32_t (&pw0)[4], const uint32_t (&pw1)[4],
+                                                 uint32_t rd, u32x4_t& a0, u32x4_t& a1) {
+    asm volatile(
+        "ds_write_b32 %2, %3\n\t"
+        "ds_write_b32 %2, %4 offset:80\n\t"
+        "ds_write_b32 %2, %5 offset:160\n\t"
+        "ds_write_b32 %2, %6 offset:240\n\t"
+        "ds_read_b128 %0, %11\n\t"
+        "ds_write_b32 %2, %7\n\t"
+        "ds_write_b32 %2, %8 offset:80\n\t"
+        "ds_write_b32 %2, %9 offset:160\n\t"
+        "ds_write_b32 %2, %10 offset:240\n\t"
+        "ds_read_b128 %1, %11\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(a0), "=&v"(a1)
+        : "v"(wr), "v"(pw0[0]), "v"(pw0[1]), "v"(pw0[2]), "v"(pw0[3]), "v"(pw1[0]), "v"(pw1[1]), "v"(pw1[2]),
+          "v"(pw1[3]), "v"(rd)
+        : "memory");
+}
+
 // Position swizzles of a page's 16-byte chunks in LDS (row = token row of
 // the page, r = page within the tile, CK chunks per row):
 // * K: chunk c of row `row` sits at position c ^ kkey(row, r), so the 16
@@ -283,7 +349,7 @@ __device__ __forceinline__ void store2_sc1(float2v_t v, const __amdgpu_buffer_rs
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), rs, off, 0, kSC1);
 }
 
-template <int HKV, bool SEG>
+template <int HKV, int GQ_, bool SEG>
 // The scalars the prologue needs come first, as separate arguments: built
 // with -mllvm -amdgpu-kernarg-preload-count=10 they arrive in SGPRs with the
 // wave, so the sequence-length and block-table loads do not wait for a
@@ -291,8 +357,9 @@ template <int HKV, bool SEG>
 __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
     const int32_t* p_seq_lens, const int32_t* p_block_table, const half_t* p_q, int p_max_chunks, int p_chunk_tiles,
     int p_bt_cols, int p_max_pages, int p_page_shift, int p_n_q_heads, int p_nblocks, Args a) {
-    using L = Geo<HKV>;
-    constexpr int D = L::D, GQ = L::GQ, G = L::G, CK = L::CK, SLOT = L::SLOT;
+    using L = Geo<HKV, GQ_>;
+    constexpr int D = L::D, GQ = L::GQ, NH = L::NH, G = L::G, CK = L::CK, SLOT = L::SLOT;
+    static_assert(GQ == 4 || GQ == 8, "4 or 8 query heads per kv head");
     constexpr uint32_t KPAGE = L::KPAGE, SPAGE = L::SPAGE;
     constexpr int PER_PAGE = L::KPAGE / 1024;  // 1 KiB loads per page of one tensor
     static_assert(kWaves == 2 * HKV && 2 * PER_PAGE == kWaves, "one K and one V load of each slot per wave");
@@ -336,14 +403,22 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
         // around the loads, so none waits for another)
         int pid0 = virtual_page(bt, min(p0 + lane, p_max_pages - 1), p_page_shift);
         int pid1 = virtual_page(bt, min(p0 + 64 + lane, p_max_pages - 1), p_page_shift);
-        // Query A operand: row n = (h, g) = (n >> 2, n & 3), nonzero only where
-        // g == jq: 32 dims of group jq of head h.
+        // Query A operand of QK MFMA m (4 of them).  GQ 4: row n = (h, g) =
+        // (n >> 2, n & 3), nonzero only where g == jq: dims 32 jq + 8 m .. + 7
+        // (group jq) of head h.  GQ 8: row n = (h, e) = (n >> 1, n & 1) and
+        // group pair P = m >> 1 (groups 2 P, 2 P + 1), nonzero only where e ==
+        // jq >> 1: dims 64 P + 16 jq + 8 (m & 1) .. + 7 (group 2 P + e).
         const half_t* qh = p_q + ((int64_t)b * p_n_q_heads + kvh * GQ) * D;
         u32x4_t qraw[4];
-        {
+        if constexpr (GQ == 4) {
             const half_t* qrow = qh + (n >> 2) * D + 32 * jq;
     #pragma unroll
             for (int m = 0; m < 4; ++m) qraw[m] = *reinterpret_cast<const u32x4_t*>(qrow + 8 * m);
+        } else {
+            const half_t* qrow = qh + (n >> 1) * D + 16 * jq;
+    #pragma unroll
+            for (int m = 0; m < 4; ++m)
+                qraw[m] = *reinterpret_cast<const u32x4_t*>(qrow + 64 * (m >> 1) + 8 * (m & 1));
         }
         asm volatile("" ::: "memory");  // keeps the loads above issued before the early return below
 
@@ -417,16 +492,19 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
 
         half8_t qa[4];
         {
-            const bool mine = (n & 3) == jq;
+            const bool mine = GQ == 4 ? (n & 3) == jq : (n & 1) == (jq >> 1);
     #pragma unroll
             for (int m = 0; m < 4; ++m) qa[m] = q_operand(mine ? qraw[m] : u32x4_t{0, 0, 0, 0});
         }
-        // Accumulator start that removes the +8 of the K codes: C row (h, g)
-        // gets -8 * 2^-24 * (sum of q over group g of head h, as the A operand
-        // holds it, high-nibble dims / 16 counted 16 times).  Lane (4 h + g, g)
-        // holds that group in qa; C lane (n, jq) needs rows (jq, 0..3).
-        float4_t init;
-        {
+        // Accumulator start that removes the +8 of the K codes: C row r gets
+        // -8 * 2^-24 * (sum of q over the row's group, as the A operand holds
+        // it, high-nibble dims / 16 counted 16 times).  GQ 4: lane (4 h + g, g)
+        // holds group g of head h in qa; C lane (n, jq) needs rows (jq, 0..3).
+        // GQ 8, pair P (accumulator init[P]): lanes (2 h + e, 2 e) and (2 h + e,
+        // 2 e + 1) hold halves of group 2 P + e of head h in qa[2 P], qa[2 P + 1];
+        // C lane (n, jq) needs rows 4 jq + i, i.e. (2 jq + (i >> 1), i & 1).
+        float4_t init[NH];
+        if constexpr (GQ == 4) {
             float part = 0.0f;
     #pragma unroll
             for (int m = 0; m < 4; ++m)
@@ -435,124 +513,215 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
             part *= -8.0f * 5.9604644775390625e-08f;
     #pragma unroll
             for (int g = 0; g < 4; ++g)
-                init[g] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
-                                                       4 * (16 * g + 4 * jq + g), __builtin_bit_cast(int, part)));
+                init[0][g] = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                          4 * (16 * g + 4 * jq + g), __builtin_bit_cast(int, part)));
+        } else {
+    #pragma unroll
+            for (int P = 0; P < 2; ++P) {
+                float part = 0.0f;
+    #pragma unroll
+                for (int m = 2 * P; m < 2 * P + 2; ++m)
+    #pragma unroll
+                    for (int i = 0; i < 8; ++i) part += (float)qa[m][i] * ((i & 2) ? 16.0f : 1.0f);
+                part *= -8.0f * 5.9604644775390625e-08f;
+    #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = 4 * jq + i, e = i & 1;
+                    const float h0 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                                   4 * (16 * (2 * e) + row), __builtin_bit_cast(int, part)));
+                    const float h1 = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                                                   4 * (16 * (2 * e + 1) + row), __builtin_bit_cast(int, part)));
+                    init[P][i] = h0 + h1;
+                }
+            }
         }
 
         // ---- per-lane LDS offsets within a slot
         // K operand of chain e: token T = 16 (n >> 3) + 4 ((n & 7) >> 1) + (n & 1) + 2 e,
-        // 16 bytes = dims [32 jq, 32 jq + 32) of head kvh.
+        // of head kvh: GQ 4, 16 bytes = dims [32 jq, 32 jq + 32); GQ 8, pair P,
+        // 8 bytes = dims [64 P + 16 jq, + 16).
         const int T0 = 16 * (n >> 3) + 4 * ((n & 7) >> 1) + (n & 1);
-        uint32_t k_off[2], ks_off[2], vs_off[2];
+        uint32_t k_off[2][NH], ks_off[2], vs_off[2];
     #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int T = T0 + 2 * e;
             const int r = T >> 4, row = T & 15;
-            k_off[e] = (uint32_t)(L::K_OFF + r * L::KPAGE + (row * CK + ((kvh * 4 + jq) ^ kkey(row, r))) * 16);
+            if constexpr (GQ == 4) {
+                k_off[e][0] = (uint32_t)(L::K_OFF + r * L::KPAGE + (row * CK + ((kvh * 4 + jq) ^ kkey(row, r))) * 16);
+            } else {
+    #pragma unroll
+                for (int P = 0; P < 2; ++P)
+                    k_off[e][P] = (uint32_t)(L::K_OFF + r * L::KPAGE +
+                                             (row * CK + ((kvh * 4 + 2 * P + (jq >> 1)) ^ kkey(row, r))) * 16 +
+                                             8 * (jq & 1));
+            }
             const int srow = row * 64 + (((kvh >> 1) ^ ((row >> 2) & 3)) * 16) + (kvh & 1) * 8;
             ks_off[e] = (uint32_t)(L::KS_OFF + r * L::SPAGE + srow);
             vs_off[e] = (uint32_t)(L::VS_OFF + r * L::SPAGE + srow);
         }
-        // Transposed V reads of group g: lane (n, jq) points at token tr_tok's
-        // 8-byte half (n & 1) of group g's chunk; after the 8 x 8 byte transpose
-        // it holds byte column n of 8 tokens (k-slot order of v_operands).
-        uint32_t tr_off[G];
+        // Transposed V reads, four a tile: lane (n, jq) points at 8 bytes of
+        // token tr_tok; after the 8 x 8 byte transpose lane n holds byte column
+        // n of 8 tokens (k-slot order of v_operands), the 16 byte columns being
+        // the bytes the lanes n & 1 = 0 and 1 point at.  GQ 4, read g: half
+        // n & 1 of group g's 16-byte chunk.  GQ 8, read 2 P + hh: half hh of the
+        // chunk of group 2 P + (n & 1), so byte column n is byte 8 hh + (n & 7)
+        // of group 2 P + (n >> 3).
+        uint32_t tr_off[4];
         {
             const int trk = n >> 1;
             const int tr_tok = 4 * jq + (trk & 3) + 16 * (trk >> 2);
     #pragma unroll
-            for (int g = 0; g < G; ++g)
-                tr_off[g] = (uint32_t)(L::V_OFF + (tr_tok >> 4) * L::KPAGE +
-                                       ((tr_tok & 15) * CK + ((kvh * 4 + g) ^ vswz<CK>(tr_tok))) * 16 + 8 * (n & 1));
+            for (int i = 0; i < 4; ++i) {
+                const int grp = GQ == 4 ? i : 2 * (i >> 1) + (n & 1);
+                const int half = GQ == 4 ? (n & 1) : (i & 1);
+                tr_off[i] = (uint32_t)(L::V_OFF + (tr_tok >> 4) * L::KPAGE +
+                                       ((tr_tok & 15) * CK + ((kvh * 4 + grp) ^ vswz<CK>(tr_tok))) * 16 + 8 * half);
+            }
         }
-        // P area of the kv head: row (h, g) = 4 h + g, 32 halves in k-slot order
-        // of the tile's token blocks (block jq' = tokens 4 jq' + i of both
-        // pages).  Lane (n, jq) writes tokens T0 and T0 + 2, k-slots
-        // 4 (n >> 3) + 2 (n & 1) and the next, of block (n & 7) >> 1 in rows
-        // (jq, 0..3); it reads row n, block jq (rows (h, g) feed the PV of group
-        // g only: the other groups' rows carry the wrong V scale and their C rows
-        // are discarded).
+        // P area of the kv head: 16 rows of 32 halves in k-slot order of the
+        // tile's token blocks (block jq' = tokens 4 jq' + i of both pages), row
+        // (h, g) = 4 h + g (GQ 4) or, for group pair P, (h, e) = 2 h + e (GQ 8,
+        // the pairs one after the other).  Lane (n, jq) writes tokens T0 and
+        // T0 + 2, k-slots 4 (n >> 3) + 2 (n & 1) and the next, of block
+        // (n & 7) >> 1 in rows 4 jq .. 4 jq + 3; it reads row n, block jq.  A row
+        // feeds the PV products of its group's dims; the C rows of the other
+        // groups carry the wrong V scale and are discarded.
         const uint32_t p_base = lds_addr(smem + L::P_OFF + kvh * L::P_AREA);
         const uint32_t p_wr =
             p_base + (uint32_t)((jq * 4) * L::P_ROW + (((n & 7) >> 1) * 8 + 4 * (n >> 3) + 2 * (n & 1)) * 2);
         const uint32_t p_rd = p_base + (uint32_t)(n * L::P_ROW + jq * 16);
 
         const float c24 = a.log2_scale * 16777216.0f;  // MFMA units -> base-2 logits
-        float m_run = -INFINITY;                       // row maximum, base-2 logits
-        float l_part = 0.0f;
-        float ps[G];  // sums of the PV weights per group (V code offset)
-        float4_t o[G][2];
+        float m_run[NH], l_part[NH];  // per query head of the lane: row maximum (base-2 logits), sum of p
+        float ps[NH][G];              // sums of the PV weights per head and group (V code offset)
+        float4_t o[4][2];             // PV accumulators: [group][lo, hi] (GQ 4), [2 P + hh][lo, hi] (GQ 8)
     #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            ps[g] = 0.0f;
-            o[g][0] = o[g][1] = float4_t{0, 0, 0, 0};
+        for (int h = 0; h < NH; ++h) {
+            m_run[h] = -INFINITY;
+            l_part[h] = 0.0f;
+    #pragma unroll
+            for (int g = 0; g < G; ++g) ps[h][g] = 0.0f;
         }
-        float t[2];     // scores (base-2 logits) of tokens T0, T0 + 2: first half -> second half
-        float mx = 0.0f;  // their row maximum
+    #pragma unroll
+        for (int i = 0; i < 4; ++i) o[i][0] = o[i][1] = float4_t{0, 0, 0, 0};
+        float t[2][NH];  // scores (base-2 logits) of tokens T0, T0 + 2: first half -> second half
+        float mx[NH];    // their row maxima
+    #pragma unroll
+        for (int h = 0; h < NH; ++h) mx[h] = 0.0f;
 
         // First half of tile `stage` (K half of its slot): scores of the lane's
-        // two tokens and the row maximum.  The two QK chains are interleaved.
+        // two tokens and the row maxima.  The QK chains are interleaved.  C lane
+        // (n, jq) holds rows 4 jq .. 4 jq + 3 of token column n: GQ 4, the four
+        // groups of head jq; GQ 8, accumulator P, groups 2 P and 2 P + 1 of heads
+        // 2 jq and 2 jq + 1.
         auto first_half = [&](int stage, uint32_t base) __attribute__((always_inline)) {
             const int tok0 = (t_begin + stage) * kTile;
-            u32x4_t kq[2];
             u32x2_t ksc[2];
-            lds_tile_reads(base + k_off[0], base + k_off[1], base + ks_off[0], base + ks_off[1], kq[0], kq[1], ksc[0],
-                           ksc[1]);
-            float4_t acc[2] = {init, init};
+            if constexpr (GQ == 4) {
+                u32x4_t kq[2];
+                lds_tile_reads(base + k_off[0][0], base + k_off[1][0], base + ks_off[0], base + ks_off[1], kq[0], kq[1],
+                               ksc[0], ksc[1]);
+                float4_t acc[2] = {init[0], init[0]};
     #pragma unroll
-            for (int e = 0; e < 2; ++e)
+                for (int e = 0; e < 2; ++e)
     #pragma unroll
-                for (int m = 0; m < 4; ++m) acc[e] = mfma16x16x32(qa[m], k_operand(kq[e][m]), acc[e]);
+                    for (int m = 0; m < 4; ++m) acc[e] = mfma16x16x32(qa[m], k_operand(kq[e][m]), acc[e]);
     #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const half2_t k01 = as_half2(ksc[e][0]), k23 = as_half2(ksc[e][1]);
-                float s = (float)k01.x * acc[e][0];
-                s = __builtin_fmaf((float)k01.y, acc[e][1], s);
-                s = __builtin_fmaf((float)k23.x, acc[e][2], s);
-                s = __builtin_fmaf((float)k23.y, acc[e][3], s);
-                // base-2 logit; s - s is 0 for a finite score and NaN for +-inf,
-                // so a non-finite K scale or query gives NaN as the eager
-                // dequantisation does, never a -inf that would drop the token
-                t[e] = __builtin_fmaf(s, c24, s - s);
+                for (int e = 0; e < 2; ++e) {
+                    const half2_t k01 = as_half2(ksc[e][0]), k23 = as_half2(ksc[e][1]);
+                    float s = (float)k01.x * acc[e][0];
+                    s = __builtin_fmaf((float)k01.y, acc[e][1], s);
+                    s = __builtin_fmaf((float)k23.x, acc[e][2], s);
+                    s = __builtin_fmaf((float)k23.y, acc[e][3], s);
+                    // base-2 logit; s - s is 0 for a finite score and NaN for +-inf,
+                    // so a non-finite K scale or query gives NaN as the eager
+                    // dequantisation does, never a -inf that would drop the token
+                    t[e][0] = __builtin_fmaf(s, c24, s - s);
+                }
+            } else {
+                u32x2_t kq[2][2];
+                lds_tile_reads8(base + k_off[0][0], base + k_off[0][1], base + k_off[1][0], base + k_off[1][1],
+                                base + ks_off[0], base + ks_off[1], kq, ksc[0], ksc[1]);
+                float4_t acc[2][2] = {{init[0], init[1]}, {init[0], init[1]}};
+    #pragma unroll
+                for (int m = 0; m < 2; ++m)
+    #pragma unroll
+                    for (int e = 0; e < 2; ++e)
+    #pragma unroll
+                        for (int P = 0; P < 2; ++P)
+                            acc[e][P] = mfma16x16x32(qa[2 * P + m], k_operand(kq[e][P][m]), acc[e][P]);
+    #pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const half2_t k01 = as_half2(ksc[e][0]), k23 = as_half2(ksc[e][1]);
+    #pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        float s = (float)k01.x * acc[e][0][2 * h];
+                        s = __builtin_fmaf((float)k01.y, acc[e][0][2 * h + 1], s);
+                        s = __builtin_fmaf((float)k23.x, acc[e][1][2 * h], s);
+                        s = __builtin_fmaf((float)k23.y, acc[e][1][2 * h + 1], s);
+                        t[e][h] = __builtin_fmaf(s, c24, s - s);  // (as above)
+                    }
+                }
             }
             if (tok0 + kTile > seq_len) {
     #pragma unroll
                 for (int e = 0; e < 2; ++e)
-                    if (tok0 + T0 + 2 * e >= seq_len) t[e] = -INFINITY;
+                    if (tok0 + T0 + 2 * e >= seq_len)
+    #pragma unroll
+                        for (int h = 0; h < NH; ++h) t[e][h] = -INFINITY;
             }
-            // row jq = head jq; its maximum is finite (token tok0 < seq_len)
-            mx = row16_max(__builtin_elementwise_maximum(t[0], t[1]));
+            // one row a head; its maximum is finite (token tok0 < seq_len) or NaN
+    #pragma unroll
+            for (int h = 0; h < NH; ++h) mx[h] = row16_max(__builtin_elementwise_maximum(t[0][h], t[1][h]));
         };
 
         // Second half of tile `stage` (V half of the next slot): online softmax
         // (lazy rescale), PV weights w = p * v_scale (one fp16 rounding), tokens
-        // T0 and T0 + 2 packed per group, and the PV products.
+        // T0 and T0 + 2 packed per row of the P area, and the PV products (GQ 8:
+        // one group pair after the other through the same P area).
         auto second_half = [&](int stage, uint32_t base) __attribute__((always_inline)) {
             const int tok0 = (t_begin + stage) * kTile;
             u32x2_t vsc[2];
-            int2v_t vw[G];
-            uint32_t tra[G];
+            int2v_t vw[4];
+            uint32_t tra[4];
     #pragma unroll
-            for (int g = 0; g < G; ++g) tra[g] = base + tr_off[g];
+            for (int i = 0; i < 4; ++i) tra[i] = base + tr_off[i];
             lds_v_reads(base + vs_off[0], base + vs_off[1], tra, vsc[0], vsc[1], vw);
-            if (__ballot(mx > m_run + kLazy) != 0) {
-                const float m_new = fmaxf(m_run, mx);
-                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-                m_run = m_new;
-                l_part *= alpha;
+            bool grow = false;
     #pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    ps[g] *= alpha;
-                    o[g][0] *= alpha;
-                    o[g][1] *= alpha;
+            for (int h = 0; h < NH; ++h) grow = grow || mx[h] > m_run[h] + kLazy;
+            if (__ballot(grow) != 0) {
+                float alpha[NH];
+    #pragma unroll
+                for (int h = 0; h < NH; ++h) {
+                    const float m_new = fmaxf(m_run[h], mx[h]);
+                    alpha[h] = __builtin_amdgcn_exp2f(m_run[h] - m_new);
+                    m_run[h] = m_new;
+                    l_part[h] *= alpha[h];
+    #pragma unroll
+                    for (int g = 0; g < G; ++g) ps[h][g] *= alpha[h];
+                }
+    #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if constexpr (GQ == 4) {
+                        o[i][0] *= alpha[0];
+                        o[i][1] *= alpha[0];
+                    } else {  // C row 4 jq + r: head 2 jq + (r >> 1)
+    #pragma unroll
+                        for (int e = 0; e < 2; ++e)
+    #pragma unroll
+                            for (int r = 0; r < 4; ++r) o[i][e][r] *= alpha[r >> 1];
+                    }
                 }
             }
-            float p[2];
+            float p[2][NH];
     #pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                p[e] = __builtin_amdgcn_exp2f(t[e] - m_run);
-                l_part += p[e];
-            }
+            for (int e = 0; e < 2; ++e)
+    #pragma unroll
+                for (int h = 0; h < NH; ++h) {
+                    p[e][h] = __builtin_amdgcn_exp2f(t[e][h] - m_run[h]);
+                    l_part[h] += p[e][h];
+                }
             float vs[2][G];
     #pragma unroll
             for (int e = 0; e < 2; ++e) {
@@ -568,22 +737,51 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
                 for (int e = 0; e < 2; ++e)
                     if (tok0 + T0 + 2 * e >= seq_len) vs[e][0] = vs[e][1] = vs[e][2] = vs[e][3] = 0.0f;
             }
-            uint32_t pw[G];
             const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+            if constexpr (GQ == 4) {
+                uint32_t pw[G];
     #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const half2_t wp = {(half_t)(p[0] * vs[0][g]), (half_t)(p[1] * vs[1][g])};
-                ps[g] = __builtin_amdgcn_fdot2(wp, one2, ps[g], false);
-                pw[g] = as_u32(wp);
-            }
-            const half8_t pa = __builtin_bit_cast(half8_t, lds_p_transpose(p_wr, pw, p_rd));
-            // group g's 32 dims as byte columns n (even dim lo, odd hi)
+                for (int g = 0; g < G; ++g) {
+                    const half2_t wp = {(half_t)(p[0][0] * vs[0][g]), (half_t)(p[1][0] * vs[1][g])};
+                    ps[0][g] = __builtin_amdgcn_fdot2(wp, one2, ps[0][g], false);
+                    pw[g] = as_u32(wp);
+                }
+                const half8_t pa = __builtin_bit_cast(half8_t, lds_p_transpose(p_wr, pw, p_rd));
+                // group g's 32 dims as byte columns n (even dim lo, odd hi)
     #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                half8_t lo, hi;
-                v_operands(vw[g], lo, hi);
-                o[g][0] = mfma16x16x32(pa, lo, o[g][0]);
-                o[g][1] = mfma16x16x32(pa, hi, o[g][1]);
+                for (int g = 0; g < G; ++g) {
+                    half8_t lo, hi;
+                    v_operands(vw[g], lo, hi);
+                    o[g][0] = mfma16x16x32(pa, lo, o[g][0]);
+                    o[g][1] = mfma16x16x32(pa, hi, o[g][1]);
+                }
+            } else {
+                uint32_t pw[2][4];  // pair P: rows 4 jq + 2 h + e, head 2 jq + h, group 2 P + e
+    #pragma unroll
+                for (int P = 0; P < 2; ++P)
+    #pragma unroll
+                    for (int h = 0; h < 2; ++h)
+    #pragma unroll
+                        for (int e = 0; e < 2; ++e) {
+                            const int g = 2 * P + e;
+                            const half2_t wp = {(half_t)(p[0][h] * vs[0][g]), (half_t)(p[1][h] * vs[1][g])};
+                            ps[h][g] = __builtin_amdgcn_fdot2(wp, one2, ps[h][g], false);
+                            pw[P][2 * h + e] = as_u32(wp);
+                        }
+                u32x4_t pa2[2];
+                lds_p_transpose2(p_wr, pw[0], pw[1], p_rd, pa2[0], pa2[1]);
+    #pragma unroll
+                for (int P = 0; P < 2; ++P) {
+                    const half8_t pa = __builtin_bit_cast(half8_t, pa2[P]);
+                    // byte columns n: bytes 8 hh + (n & 7) of group 2 P + (n >> 3)
+    #pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        half8_t lo, hi;
+                        v_operands(vw[2 * P + hh], lo, hi);
+                        o[2 * P + hh][0] = mfma16x16x32(pa, lo, o[2 * P + hh][0]);
+                        o[2 * P + hh][1] = mfma16x16x32(pa, hi, o[2 * P + hh][1]);
+                    }
+                }
             }
         };
 
@@ -622,22 +820,51 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
         __syncthreads();
 
         // ---- each set's (m, l, o) of kv head kvh in LDS area `wave`:
-        // [0, 4) m, [4, 8) l, [8 + h D, ...) o (unnormalised, code offset removed).
+        // [0, GQ) m, [GQ, 2 GQ) l, [2 GQ + h D, ...) o (unnormalised, code
+        // offset removed); lane (n, jq) holds heads NH jq .. NH jq + NH - 1.
         {
-            l_part = row16_sum(l_part);
-            float psr[G];
+            float psr[NH][G];
     #pragma unroll
-            for (int g = 0; g < G; ++g) psr[g] = 8.0f * row16_sum(ps[g]);
+            for (int h = 0; h < NH; ++h) {
+                l_part[h] = row16_sum(l_part[h]);
+    #pragma unroll
+                for (int g = 0; g < G; ++g) psr[h][g] = 8.0f * row16_sum(ps[h][g]);
+            }
             float* const ep = reinterpret_cast<float*>(smem + wave * L::EPI_AREA);
             if (n == 0) {
-                ep[jq] = m_run;
-                ep[4 + jq] = l_part;
+    #pragma unroll
+                for (int h = 0; h < NH; ++h) {
+                    ep[NH * jq + h] = m_run[h];
+                    ep[GQ + NH * jq + h] = l_part[h];
+                }
             }
+            if constexpr (GQ == 4) {
     #pragma unroll
-            for (int g = 0; g < G; ++g)
+                for (int g = 0; g < G; ++g)
     #pragma unroll
-                for (int e = 0; e < 2; ++e)
-                    ep[8 + jq * D + 32 * g + 2 * n + e] = o[g][e][g] * (e ? 1048576.0f : 16777216.0f) - psr[g];
+                    for (int e = 0; e < 2; ++e)
+                        ep[2 * GQ + jq * D + 32 * g + 2 * n + e] =
+                            o[g][e][g] * (e ? 1048576.0f : 16777216.0f) - psr[0][g];
+            } else {
+                // accumulator 2 P + hh, column n: dims 16 hh + 2 (n & 7) (+ 1 for
+                // hi) of group 2 P + (n >> 3), kept in C rows of that group: 2 h +
+                // (n >> 3) for head 2 jq + h
+                const bool odd = (n >> 3) != 0;
+    #pragma unroll
+                for (int P = 0; P < 2; ++P)
+    #pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+    #pragma unroll
+                        for (int e = 0; e < 2; ++e)
+    #pragma unroll
+                            for (int h = 0; h < 2; ++h) {
+                                const float4_t c = o[2 * P + hh][e];
+                                const float v = odd ? c[2 * h + 1] : c[2 * h];
+                                const float off = odd ? psr[h][2 * P + 1] : psr[h][2 * P];
+                                ep[2 * GQ + (2 * jq + h) * D + 32 * (2 * P + (n >> 3)) + 16 * hh + 2 * (n & 7) + e] =
+                                    v * (e ? 1048576.0f : 16777216.0f) - off;
+                            }
+            }
         }
         __syncthreads();
 
@@ -653,9 +880,9 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
             const float* w1 = reinterpret_cast<const float*>(smem + (HKV + j) * L::EPI_AREA);
             m = fmaxf(w0[h], w1[h]);
             const float a0 = __builtin_amdgcn_exp2f(w0[h] - m), a1 = __builtin_amdgcn_exp2f(w1[h] - m);
-            l = w0[4 + h] * a0 + w1[4 + h] * a1;
-            const float4_t o0 = *reinterpret_cast<const float4_t*>(w0 + 8 + h * D + d);
-            const float4_t o1 = *reinterpret_cast<const float4_t*>(w1 + 8 + h * D + d);
+            l = w0[GQ + h] * a0 + w1[GQ + h] * a1;
+            const float4_t o0 = *reinterpret_cast<const float4_t*>(w0 + 2 * GQ + h * D + d);
+            const float4_t o1 = *reinterpret_cast<const float4_t*>(w1 + 2 * GQ + h * D + d);
             return (o0 * a0 + o1 * a1) * (1.0f / l);
         };
         const int64_t out_base = (int64_t)b * total;
@@ -676,7 +903,7 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
             return;
         }
 
-        if constexpr (!SEG) {
+        if constexpr (!SEG && GQ == 4) {
             // Chunk mode: at most 64 chunks a sequence, merged in one level.
             // ---- split-KV: publish (o / l, m, l) with device-coherent stores; the
             // last chunk to arrive merges every chunk of the sequence.
@@ -745,13 +972,16 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
                 store_out4(e4, acc * (1.0f / lsum));
             }
         } else {
-            // Balanced mode: up to 8 x 64 chunks a sequence, two levels.
+            // Balanced mode (up to 8 x 64 chunks a sequence) and chunk mode at
+            // GQ 8 (up to 64 chunks, partials of 32 KiB at 64 query heads): two
+            // levels, in groups of MG chunks.
             // ---- split-KV: publish (o / l, m, l) with device-coherent stores; the
-            // last chunk of each group of kMergeGroup chunks to arrive merges the
-            // group; with more than one group, the group partials go out the same
-            // way and the last group to arrive merges them (two levels, so no
-            // workgroup reads more than kMergeGroup chunk partials or kMaxGroups
-            // group partials).
+            // last chunk of each group of MG chunks to arrive merges the group;
+            // with more than one group, the group partials go out the same way
+            // and the last group to arrive merges them (two levels, so no
+            // workgroup reads more than MG chunk partials or kMaxGroups group
+            // partials).
+            constexpr int MG = SEG ? kMergeGroup : kMergeGroup8;
             const uint32_t part_o = (uint32_t)total * 4, part_ml = (uint32_t)hq * 8;  // bytes per partial
             {
                 const auto ro = buf_rsrc(a.part_o + (row0 + chunk) * total, part_o);
@@ -830,12 +1060,12 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
                     }
                 }
             };
-            const int grp = chunk / kMergeGroup;
-            const int n_groups = (n_chunks + kMergeGroup - 1) / kMergeGroup;
-            const int members = min(kMergeGroup, n_chunks - grp * kMergeGroup);
+            const int grp = chunk / MG;
+            const int n_groups = (n_chunks + MG - 1) / MG;
+            const int members = min(MG, n_chunks - grp * MG);
             if (!arrive(seq_ctr + grp, members)) return;
-            const int64_t c0row = row0 + grp * kMergeGroup;
-            merge(a.part_o + c0row * total, a.part_ml + c0row * hq * 2, members, chunk - grp * kMergeGroup, n_groups == 1,
+            const int64_t c0row = row0 + grp * MG;
+            merge(a.part_o + c0row * total, a.part_ml + c0row * hq * 2, members, chunk - grp * MG, n_groups == 1,
                   a.grp_o + (row0 + grp) * total, a.grp_ml + (row0 + grp) * hq * 2);
             if (n_groups == 1) return;
             wait_vmcnt<0>();
@@ -896,7 +1126,7 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
             // tokens): a range would not fit the page-id window.  Every
             // workgroup sees the same C, so all of them write NaN into the
             // whole output instead of a wrong result.
-            const int64_t n_out = (int64_t)a.batch * p_n_q_heads * Geo<HKV>::D;
+            const int64_t n_out = (int64_t)a.batch * p_n_q_heads * D;
             for (int64_t i = (int64_t)blockIdx.x * (64 * kWaves) + threadIdx.x; i < n_out;
                  i += (int64_t)gridDim.x * (64 * kWaves)) {
                 if (a.out_f32) reinterpret_cast<float*>(a.out)[i] = __builtin_nanf("");
@@ -967,21 +1197,21 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
 
 namespace {
 
-template <int HKV>
+template <int HKV, int GQ>
 int stream_lds_bytes() {
-    using L = st::Geo<HKV>;
+    using L = st::Geo<HKV, GQ>;
     const int epi = 2 * HKV * L::EPI_AREA + 16;
     return L::LDS_MAIN > epi ? L::LDS_MAIN : epi;
 }
 
-template <int HKV, bool SEG>
+template <int HKV, int GQ, bool SEG>
 int launch_stream(dim3 grid, hipStream_t s, const st::Args& a) {
-    const int lds = stream_lds_bytes<HKV>();
+    const int lds = stream_lds_bytes<HKV, GQ>();
     if (lds > kMaxLdsBytes) return kInvalidArgument;
     static std::atomic<uint64_t> lds_raised{0};
-    if (allow_full_lds(reinterpret_cast<const void*>(&st::int4_decode_stream_kernel<HKV, SEG>), lds_raised) != kOk)
+    if (allow_full_lds(reinterpret_cast<const void*>(&st::int4_decode_stream_kernel<HKV, GQ, SEG>), lds_raised) != kOk)
         return kLaunchError;
-    hipLaunchKernelGGL((st::int4_decode_stream_kernel<HKV, SEG>), grid, dim3(64 * st::kWaves), lds, s, a.seq_lens, a.block_table, a.q,
+    hipLaunchKernelGGL((st::int4_decode_stream_kernel<HKV, GQ, SEG>), grid, dim3(64 * st::kWaves), lds, s, a.seq_lens, a.block_table, a.q,
                        a.max_chunks, a.chunk_tiles, a.bt_cols, a.max_pages, a.page_shift, a.n_q_heads, (int)grid.x, a);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchError;
 }
@@ -991,7 +1221,17 @@ int launch_stream(dim3 grid, hipStream_t s, const st::Args& a) {
 int stream_max_chunks() { return st::kMaxChunks; }
 
 bool stream_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim) {
+    return head_dim == 128 && num_kv_heads == 8 && (num_q_heads == 4 * num_kv_heads || num_q_heads == 8 * num_kv_heads);
+}
+
+bool stream_balanced_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim) {
     return head_dim == 128 && num_kv_heads == 8 && num_q_heads == 4 * num_kv_heads;
+}
+
+// Chunk mode merges in one level at 4 query heads per kv head, in groups of
+// kMergeGroup8 at 8.
+static bool chunk_two_level(int64_t num_q_heads, int64_t num_kv_heads, int64_t max_chunks) {
+    return num_q_heads == 8 * num_kv_heads && max_chunks > st::kMergeGroup8;
 }
 
 // Split-KV workspace: [counters][chunk partials o][chunk (m, l)] and, when a
@@ -1033,8 +1273,11 @@ int stream_balanced_plan(int64_t batch, int64_t num_q_heads, int64_t head_dim, i
     return kOk;
 }
 
-int64_t stream_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t max_chunks) {
-    return stream_workspace(batch, num_q_heads, head_dim, batch * max_chunks, false).total;  // chunk mode: one level
+int64_t stream_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                               int64_t max_chunks) {
+    return stream_workspace(batch, num_q_heads, head_dim, batch * max_chunks,
+                            chunk_two_level(num_q_heads, num_kv_heads, max_chunks))
+        .total;
 }
 
 int stream_launch(const void* query, const void* k_data, const void* v_data, const void* k_scale, const void* v_scale,
@@ -1043,12 +1286,14 @@ int stream_launch(const void* query, const void* k_data, const void* v_data, con
                   int64_t num_kv_heads, int64_t head_dim, int64_t max_pages, int64_t bt_cols, int32_t page_shift,
                   float softmax_scale, int32_t chunk_tiles, int32_t max_chunks, void* stream) {
     if (!stream_supported(num_q_heads, num_kv_heads, head_dim)) return kInvalidArgument;
+    const bool gq8 = num_q_heads == 8 * num_kv_heads;
     // chunk_tiles > 0: chunk mode, batch x max_chunks workgroups; < 0: the
     // balanced mode, max_chunks ranges of at most -chunk_tiles units, a
     // workgroup each (stream_balanced_plan).
     const bool balanced = chunk_tiles < 0;
     const int64_t share = balanced ? -(int64_t)chunk_tiles : chunk_tiles;
     if (share <= 0 || share > st::kMaxChunkTiles || max_chunks <= 0) return kInvalidArgument;
+    if (balanced && gq8) return kInvalidArgument;  // (balanced mode: 4 query heads per kv head)
     if (balanced ? max_chunks > st::kMergeGroup * st::kMaxGroups : max_chunks > st::kMaxChunks) return kInvalidArgument;
     if (!balanced && share * max_chunks * 2 < max_pages) return kInvalidArgument;  // the grid covers every page
     const int64_t nblocks = balanced ? max_chunks : batch * (int64_t)max_chunks;
@@ -1076,7 +1321,8 @@ int stream_launch(const void* query, const void* k_data, const void* v_data, con
     if (max_chunks > 1) {  // (one balanced range: every piece is a whole sequence)
         const StreamWorkspace w = balanced ? stream_workspace(batch, num_q_heads, head_dim, max_chunks + batch,
                                                               max_chunks > st::kMergeGroup)
-                                           : stream_workspace(batch, num_q_heads, head_dim, batch * max_chunks, false);
+                                           : stream_workspace(batch, num_q_heads, head_dim, batch * max_chunks,
+                                                              chunk_two_level(num_q_heads, num_kv_heads, max_chunks));
         if (workspace == nullptr || workspace_bytes_avail < w.total) return kWorkspaceTooSmall;
         uint8_t* const ws = (uint8_t*)workspace;
         a.counters = (uint32_t*)ws;
@@ -1085,8 +1331,9 @@ int stream_launch(const void* query, const void* k_data, const void* v_data, con
         a.grp_o = (float*)(ws + w.grp_o);
         a.grp_ml = (float*)(ws + w.grp_ml);
     }
-    if (balanced) return launch_stream<8, true>(dim3((unsigned)nblocks), (hipStream_t)stream, a);
-    return launch_stream<8, false>(dim3((unsigned)nblocks), (hipStream_t)stream, a);
+    if (balanced) return launch_stream<8, 4, true>(dim3((unsigned)nblocks), (hipStream_t)stream, a);
+    if (gq8) return launch_stream<8, 8, false>(dim3((unsigned)nblocks), (hipStream_t)stream, a);
+    return launch_stream<8, 4, false>(dim3((unsigned)nblocks), (hipStream_t)stream, a);
 }
 
 }  // namespace iris

@@ -8,7 +8,7 @@ from pathlib import Path
 import pytest
 
 from iris_kernel import _lib
-from iris_kernel.fused_attention import decode_plan, fp16_decode_plan
+from iris_kernel.fused_attention import DECODE_PAGE_KERNEL, decode_plan, fp16_decode_plan
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "iris_hip.h"
 
@@ -170,7 +170,7 @@ def pages_workspace(B, Hq, D, max_chunks, balanced=False):
     # (B, Hq, Hkv, D, maxP, total, max)
     ((32, 32, 8, 128, 256, 32 * 4096, 4096), True, True),      # Llama-3-8B shape: page kernel
     ((64, 32, 8, 128, 1024, 64 * 3000, 16384), True, True),    # ragged batch: page kernel, balanced mode
-    ((4, 64, 8, 128, 8192, 4 * 131072, 131072), True, False),  # 8 query heads per kv head: general
+    ((4, 64, 8, 128, 8192, 4 * 131072, 131072), True, True),   # 8 query heads per kv head: streaming kernel
     ((4, 8, 2, 64, 16, 400, 200), False, False),               # D = 64: general; tiny grid, one chunk
     ((8, 32, 8, 128, 512, 8 * 8192, 8192), True, False),       # 75 MB of K/V: general kernel
 ])
@@ -193,6 +193,24 @@ def test_decode_plan_covers_every_tile(cfg, expect_chunks, expect_pages):
         assert ws == pages_workspace(B, Hq, D, max_chunks)
     else:
         assert ws == general_workspace(B, Hq, Hkv, D, max_chunks, maxP)
+
+
+def test_gqa8_plans():
+    # 8 query heads per kv head (D=128, Hkv=8): the streaming kernel has a
+    # chunk mode only, so 16-wave requests get chunk plans even for ragged
+    # lengths; the page-kernel bit keeps the page kernel's balanced mode; a
+    # block table wider than 64 chunks of 64 tiles leaves the plan's choice to
+    # the general kernel; a short batch too.
+    B, Hq, Hkv, D = 4, 64, 8, 128
+    ct, mc, nw, ws = decode_plan(B, Hq, Hkv, D, 8192, B * 131072, 131072)
+    assert (ct, mc, nw) == (64, 64, 16) and ws == pages_workspace(B, Hq, D, 64)
+    ct, mc, nw, _ = decode_plan(B, Hq, Hkv, D, 8192, 131072 + 3 * 5000, 131072, waves_per_block=16)
+    assert ct > 0 and mc <= 64 and nw == 16
+    ct, mc, nw, _ = decode_plan(B, Hq, Hkv, D, 8192, 131072 + 3 * 5000, 131072,
+                                waves_per_block=16 | DECODE_PAGE_KERNEL)
+    assert ct < 0 and nw == 16 | DECODE_PAGE_KERNEL
+    assert decode_plan(B, Hq, Hkv, D, 8193, B * 131072, 131072)[2] <= 4
+    assert decode_plan(B, Hq, Hkv, D, 64, B * 1024, 1024)[2] <= 4
 
 
 @pytest.mark.parametrize("cfg", [

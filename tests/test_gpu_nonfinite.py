@@ -13,7 +13,8 @@ finite values within the attention tolerance.  (Where the eager result is
 the codes' +8 offset by a second sum, give NaN: both are non-finite.)
 
 Each case is run on the plan's own choice, on each INT4 kernel forced (the
-streaming kernel at its shape, the MQA kernel at its shape, the page kernel,
+streaming kernel at its shapes (4 and 8 query heads per kv head), the MQA
+kernel at its shape, the page kernel,
 the general kernel and its VALU tile, the any-shape kernel, which a head_dim
 of 96 selects by itself), with one chunk a sequence and with
 split-KV, and on a cache the package's own append wrote from an infinite key
@@ -43,6 +44,9 @@ KERNELS = [
     ("gqa-pages", 32, 8, 128, 16 | DECODE_PAGE_KERNEL),
     ("gqa-general", 32, 8, 128, 4),
     ("gqa-valu", 32, 8, 128, 4 | DECODE_VALU_TILE),
+    ("gqa8-stream", 64, 8, 128, 16),
+    ("gqa8-pages", 64, 8, 128, 16 | DECODE_PAGE_KERNEL),
+    ("gqa8-general", 64, 8, 128, 4),
     ("mqa-auto", 16, 1, 64, 0),
     ("mqa-mqa", 16, 1, 64, 16),
     ("mqa-pages", 16, 1, 64, 16 | DECODE_PAGE_KERNEL),
