@@ -238,11 +238,17 @@ int iris_int4_paged_decode_attention_noalloc(const void *query, const void *k_da
 
 /*
  * Split plan for iris_fp16_paged_decode_attention (no reference counterpart;
- * see iris_decode_plan): pages per chunk (out_chunk_pages, at most 256),
- * chunks per (sequence, kv head) for the widest block_table
- * (out_max_chunks, at most 512) and the workspace size in bytes (0 when no
- * sequence can need more than one chunk).  total_tokens and max_tokens may
- * be -1 if unknown; tokens_per_split > 0 overrides the heuristic.
+ * see iris_decode_plan): pages per chunk (out_chunk_pages), chunks per
+ * sequence for the widest block_table (out_max_chunks) and the workspace
+ * size in bytes (0 when no sequence can need more than one chunk).
+ * total_tokens and max_tokens may be -1 if unknown (the widest batch
+ * block_table admits stands in); tokens_per_split > 0 steers the chunk size.
+ * Two kernels: a negative out_chunk_pages (chunks of -out_chunk_pages <= 128
+ * pages, at most 16 a sequence) selects the page-streaming kernel (head_dim
+ * 128 with 4 or 8 kv heads, head_dim 64 with 8 or 16, batches of similar
+ * lengths: 4 * total_tokens >= 3 * batch * max_tokens); a positive one the
+ * per-kv-head kernel (at most 256 pages a chunk, at most 512 chunks per
+ * (sequence, kv head)).
  */
 int iris_fp16_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                           int64_t max_pages, int64_t total_tokens, int64_t max_tokens,
@@ -268,7 +274,8 @@ int iris_fp16_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_hea
  *                before the first call and before a call whose batch exceeds
  *                the previous call's.  Calls sharing a workspace must not
  *                overlap in time.
- *   chunk_pages, max_chunks: from iris_fp16_decode_plan
+ *   chunk_pages, max_chunks: from iris_fp16_decode_plan (the sign of
+ *                chunk_pages selects the kernel)
  *
  * page_size must be 16, head_dim 64 or 128, num_q_heads / num_kv_heads at
  * most 16 (fused_attention.py:390-403).  16-byte alignment is required for

@@ -40,6 +40,7 @@
 #include <cstdlib>
 
 #include "common.h"
+#include "decode_fp16_stream.h"
 #include "iris_hip.h"
 
 namespace iris {
@@ -407,9 +408,14 @@ int64_t f16_workspace_bytes(int64_t batch, int64_t hq, int64_t hkv, int64_t head
 
 using namespace iris;
 
-// Split plan of the FP16 decode: pages per chunk, chunks per (sequence, kv
-// head) and workspace bytes.  About 1024 workgroups (four per CU), at least
-// 8 pages (two per wave) each; one chunk when the longest sequence fits.
+// Split plan of the FP16 decode: pages per chunk, chunks per sequence and
+// workspace bytes.  The page-streaming kernel (decode_fp16_stream.hip) takes
+// its shapes for batches of similar lengths (unknown lengths count as the
+// widest batch), with about one workgroup of all kv heads a CU; its plan has
+// a negative chunk_pages.  Ragged batches and the other shapes get the
+// per-kv-head kernel's plan: about 1024 workgroups (four per CU), at least 8
+// pages (two per wave) each; one chunk when the longest sequence fits.  Both
+// kernels' workspaces have the same size for the same chunk count.
 extern "C" int iris_fp16_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
                                      int64_t head_dim, int64_t max_pages, int64_t total_tokens,
                                      int64_t max_tokens, int32_t tokens_per_split, int32_t* out_chunk_pages,
@@ -420,6 +426,17 @@ extern "C" int iris_fp16_decode_plan(int64_t batch, int64_t num_q_heads, int64_t
     const int64_t cap_tokens = max_pages * f16::kPage;
     if (max_tokens < 0 || max_tokens > cap_tokens) max_tokens = cap_tokens;
     if (total_tokens < 0) total_tokens = batch * max_tokens;
+    // (the page-streaming kernel's chunks are at most 16 a sequence: with
+    // ragged lengths the long sequences' chunks would outlast the rest;
+    // MI355X, configuration 3: 345 us against 235)
+    if (fp16_stream_supported(num_q_heads, num_kv_heads, head_dim) && 4 * total_tokens >= 3 * batch * max_tokens &&
+        fp16_stream_plan(batch, max_pages, total_tokens, max_tokens, tokens_per_split, out_chunk_pages,
+                         out_max_chunks) == kOk) {
+        *out_workspace_bytes =
+            *out_max_chunks > 1 ? fp16_stream_workspace_bytes(batch, num_q_heads, head_dim, *out_max_chunks) : 0;
+        *out_chunk_pages = -*out_chunk_pages;  // negative: the page-streaming kernel
+        return kOk;
+    }
     int64_t chunk_pages;
     if (tokens_per_split > 0) {
         chunk_pages = (tokens_per_split + f16::kPage - 1) / f16::kPage;
@@ -461,6 +478,14 @@ extern "C" int iris_fp16_paged_decode_attention(const void* query, const void* k
     if (page_size != f16::kPage || batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
         num_q_heads / num_kv_heads > 16 || (head_dim != 64 && head_dim != 128) || max_pages <= 0)
         return kInvalidArgument;
+    // A negative chunk_pages: the page-streaming kernel's plan.
+    if (chunk_pages < 0) {
+        const int64_t cp = -(int64_t)chunk_pages;
+        if (cp > 0x7FFFFFFF) return kInvalidArgument;
+        return fp16_stream_launch(query, k_cache, v_cache, block_table, seq_lens, output, output_is_f32, workspace,
+                                  workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, max_pages,
+                                  softmax_scale, (int32_t)cp, max_chunks, stream);
+    }
     if (chunk_pages <= 0 || chunk_pages > f16::kMaxChunkPages || max_chunks <= 0 || max_chunks > f16::kMaxMergeChunks ||
         (int64_t)chunk_pages * max_chunks < max_pages)
         return kInvalidArgument;

@@ -33,6 +33,7 @@ SOURCES = {
     "decode_mqa.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
     "decode_any.hip": [],
     "decode_fp16.hip": [],
+    "decode_fp16_stream.hip": [],
     "kv_fp16.hip": ["-ffp-contract=off"],
     "check.hip": [],
 }

@@ -116,8 +116,14 @@ def test_fp16_and_write_side_entry_points_reject_bad_arguments_before_launch():
 
 
 def test_fp16_decode_plan():
+    # configuration 2's shape and lengths: the page-streaming kernel (negative
+    # chunk_pages), chunks of all kv heads, one workgroup a CU
     cp, mc, ws = fp16_decode_plan(32, 32, 8, 128, 256, 32 * 4096, 4096)
-    assert cp * mc >= 256 and cp * (mc - 1) < 256 and cp <= 256
+    assert cp < 0 and -cp * mc >= 256 and -cp * (mc - 1) < 256 and -cp <= 128 and mc <= 16
+    assert 32 * mc == 256 and ws > 0
+    # ragged lengths: the per-kv-head kernel
+    cp, mc, ws = fp16_decode_plan(32, 32, 8, 128, 256, 16 * 4096, 4096)
+    assert cp > 0 and cp * mc >= 256 and cp * (mc - 1) < 256 and cp <= 256
     assert mc > 1 and ws > 0
     # one chunk when the longest sequence fits in one (here 4 pages < 8)
     cp, mc, ws = fp16_decode_plan(4, 8, 2, 64, 4, 200, 60)

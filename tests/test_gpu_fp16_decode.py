@@ -171,6 +171,43 @@ def test_fp16_gqa_ratios_and_head_dims(device, hq, hkv, d):
         assert_attention_close(out, want, f"fp16 hq={hq} hkv={hkv} d={d} tps={tps}")
 
 
+# The page-streaming kernel (decode_fp16_stream.hip: head_dim 128 with 4 or 8
+# kv heads, head_dim 64 with 8 or 16; the plan's choice there for batches of
+# similar lengths and for unknown lengths, so these ragged batches take its
+# plan from the block table's width): partial tiles and pages, one-token
+# sequences, one to 16 chunks, 4 to 16 query heads per kv head, both output
+# types.
+@pytest.mark.parametrize("hq,hkv,d,lens,tps", [
+    (32, 8, 128, [1, 9, 16, 17, 300, 2049], 0),
+    (32, 8, 128, [1, 9, 16, 17, 300, 2049], 128),   # 8-page chunks (16 a sequence at most)
+    (16, 4, 128, [5000, 33], 1024),
+    (64, 8, 128, [3000, 8], 256),                    # 8 query heads per kv head
+    (128, 8, 64, [700, 1500], 0),                    # head_dim 64, 16 per kv head
+    (16, 16, 64, [40, 2000, 777], 512),              # 16 kv heads
+])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+def test_fp16_page_streaming_kernel_matches_eager(device, hq, hkv, d, lens, tps, out_dtype):
+    from iris_kernel.fused_attention import _launch_fp16_decode, fp16_decode_plan
+    g = torch.Generator().manual_seed(hq + hkv + d + len(lens) + tps)
+    B = len(lens)
+    maxp = max(-(-n // 16) for n in lens) + 1
+    NP = B * maxp + 2
+    bt = torch.randperm(NP, generator=g)[: B * maxp].view(B, maxp).to(torch.int32)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    kc = torch.randn(NP, 16, hkv, d, generator=g).to(torch.float16)
+    vc = torch.randn(NP, 16, hkv, d, generator=g).to(torch.float16)
+    q = torch.randn(B, hq, d, generator=g).to(torch.float16)
+    plan = fp16_decode_plan(B, hq, hkv, d, maxp, -1, -1, tps)
+    assert -128 <= plan[0] < 0 and plan[1] <= 16, plan  # the page-streaming kernel's plan
+    assert fp16_decode_plan(B, hq, hkv, d, maxp, sum(lens), max(lens), tps)[0] > 0  # ragged: the other kernel
+    want = torch_eager_fp16_paged_decode_attention(q, kc, vc, bt, sl, out_dtype=torch.float32)
+    out = torch.empty(B, hq, d, dtype=out_dtype, device=device)
+    _launch_fp16_decode(*to(device, q, kc, vc, bt, sl), out, d ** -0.5, plan)
+    torch.cuda.synchronize(device)
+    assert_attention_close(out, want if out_dtype == torch.float32 else want.to(torch.float16),
+                           f"fp16 stream hq={hq} hkv={hkv} d={d} lens={lens} tps={tps} plan={plan}")
+
+
 def test_fp16_softmax_scale_and_private_handle(device):
     case, cpu, gpu = prepared(1, device)
     want = eager(case, cpu, softmax_scale=0.3)
