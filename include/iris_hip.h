@@ -144,9 +144,9 @@ int iris_quantize_pack_int4(const void *x, void *packed, void *scales, int64_t n
  * that is a multiple of 32 up to 512 and every page size, with fp32
  * dequantisation as the eager path does it.  iris_decode_plan sets it by
  * itself for head dims other than 64, 128 and 256; a caller whose page size
- * is not 16 << k (16-256) must ask for it (the plan is not told the page
- * size), and iris_int4_paged_decode_attention refuses such a page size
- * without it.  At most one selection bit may be set. */
+ * is not a multiple of 16 up to 256 must ask for it (the plan is not told
+ * the page size), and iris_int4_paged_decode_attention refuses such a page
+ * size without it.  At most one selection bit may be set. */
 #define IRIS_DECODE_ANY_KERNEL 0x400
 int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                      int64_t max_pages, int64_t total_tokens, int64_t max_tokens,
@@ -195,8 +195,8 @@ int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, i
  * any num_q_heads / num_kv_heads, as the eager path takes them
  * (torch_eager_attention.py:72, :93; the reference's fused path takes
  * page_size 16, head_dim 64 or 128 and at most 16 query heads per kv head,
- * fused_attention.py:390-403).  Page sizes other than 16 << k (16-256)
- * need a plan made with IRIS_DECODE_ANY_KERNEL.  max_pages is the number of
+ * fused_attention.py:390-403).  Page sizes that are not a multiple of 16
+ * up to 256 need a plan made with IRIS_DECODE_ANY_KERNEL.  max_pages is the number of
  * block_table columns; plan with ceil(max_pages * page_size / 16).
  * Page ids and lengths are not
  * range-checked on the device (fused_attention.py:415-429 does that on the

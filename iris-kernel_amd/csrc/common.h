@@ -133,13 +133,17 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expect) 
     return last;
 }
 
-// Pages of page_size = 16 << page_shift tokens are read as 1 << page_shift
-// consecutive 16-token pages (the [num_pages, page_size, ...] cache is the
-// same bytes as a [num_pages << page_shift, 16, ...] one): virtual 16-token
-// page vp of a block-table row is 16-token page
-// (row[vp >> page_shift] << page_shift) + (vp & ((1 << page_shift) - 1)).
-__device__ __forceinline__ int virtual_page(const int32_t* row, int vp, int page_shift) {
-    return (row[vp >> page_shift] << page_shift) | (vp & ((1 << page_shift) - 1));
+// Pages of page_size = 16 m tokens are read as m consecutive 16-token pages
+// (the [num_pages, page_size, ...] cache is the same bytes as a
+// [num_pages * m, 16, ...] one): virtual 16-token page vp of a block-table
+// row is 16-token page row[vp / m] * m + vp % m.  page_code is log2(m) when
+// m is a power of two (a shift) and -m otherwise (a division, once per lane
+// in a kernel's prologue); a kernel argument, so the branch is uniform.
+__device__ __forceinline__ int virtual_page(const int32_t* row, int vp, int page_code) {
+    if (page_code >= 0) return (row[vp >> page_code] << page_code) | (vp & ((1 << page_code) - 1));
+    const int m = -page_code;
+    const int e = vp / m;
+    return row[e] * m + (vp - e * m);
 }
 
 // LDS a workgroup may use on gfx950 (per CU).

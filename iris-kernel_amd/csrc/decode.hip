@@ -100,7 +100,7 @@ struct DecodeArgs {
     int out_f32;
     int batch, n_q_heads, n_kv_heads, group;  // group = Hq / Hkv
     int max_pages;            // 16-token pages a block-table row addresses
-    int bt_cols, page_shift;  // block-table columns; page_size = 16 << page_shift
+    int bt_cols, page_shift;  // block-table columns; the page code of virtual_page (page_size = 16 m)
     // kv blocks: (KVW kv heads) x (q_blocks blocks of 16 of a kv head's
     // query heads; q_blocks > 1 only for group > 16, with KVW = 1)
     int n_kv_blocks, q_blocks, max_chunks, chunk_tiles;
@@ -1373,7 +1373,7 @@ constexpr int64_t kPagesMinBytes = 100000000;  // K/V bytes above which the page
 // workgroup per CU balances ragged batches worse than the general kernel's
 // many small ones) that read at least kPagesMinBytes of K/V.
 // Shapes none of these kernels has -- head_dim other than 64, 128 or 256,
-// page sizes other than 16 << k -- run on the any-shape kernel
+// page sizes that are not multiples of 16 (or past 256) -- run on the any-shape kernel
 // (decode_any.hip), named by a third bit, IRIS_DECODE_ANY_KERNEL: the plan
 // sets it for such head dims by itself; for such page sizes (which the
 // plan is not told) the caller asks for it, and a launch with such a page
@@ -1543,16 +1543,18 @@ extern "C" int iris_int4_paged_decode_attention(
         return any_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
                           workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, page_size,
                           max_pages, softmax_scale, chunk_tiles, max_chunks, stream);
-    // page_size = 16 << shift: each table entry stands for 1 << shift
-    // consecutive 16-token pages, so the kernels see max_pages << shift of
-    // them per row (the count the plan was made with).
-    int shift = 0;
-    while (shift < 5 && (kPageSize << shift) != page_size) ++shift;
-    if (shift == 5 || batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
-        !fast_head_dim(head_dim) || max_pages <= 0 || (max_pages << shift) > 0x3FFFFFFF)
+    // page_size = 16 m (m at most 16): each table entry stands for m
+    // consecutive 16-token pages, so the kernels see max_pages * m of them
+    // per row (the count the plan was made with); they take the page code
+    // log2(m) for a power of two, else -m (virtual_page in common.h).
+    if (page_size < kPageSize || page_size > 16 * kPageSize || page_size % kPageSize != 0 || batch <= 0 ||
+        num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || !fast_head_dim(head_dim) || max_pages <= 0 ||
+        max_pages * (page_size / kPageSize) > 0x3FFFFFFF)
         return kInvalidArgument;
+    const int page_mul = (int)(page_size / kPageSize);
+    const int shift = (page_mul & (page_mul - 1)) == 0 ? __builtin_ctz((unsigned)page_mul) : -page_mul;
     const int64_t bt_cols = max_pages;
-    max_pages <<= shift;
+    max_pages *= page_mul;
     const int32_t waves = waves_of(waves_per_block);
     if (waves == mqa_waves() && mqa_allowed(waves_per_block) &&
         mqa_supported(num_q_heads, num_kv_heads, head_dim) && chunk_tiles > 0)

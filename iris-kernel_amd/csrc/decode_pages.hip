@@ -113,7 +113,7 @@ struct Args {
     int out_f32;
     int batch, n_q_heads, n_kv_heads, group;  // group = Hq / Hkv
     int max_pages;                // 16-token pages a block-table row addresses
-    int bt_cols, page_shift;      // block-table columns; page_size = 16 << page_shift
+    int bt_cols, page_shift;      // block-table columns; the page code of virtual_page (page_size = 16 m)
     int max_chunks, chunk_tiles;  // chunk mode: workgroup (b, chunk), b * max_chunks + chunk
     int segmented;                // balanced mode: workgroup w takes tiles [w T / W, (w + 1) T / W)
     int slots;                    // workgroups + B

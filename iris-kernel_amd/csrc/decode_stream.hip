@@ -166,7 +166,7 @@ struct Args {
     int out_f32;
     int batch, n_q_heads, max_chunks, chunk_tiles;
     int max_pages;            // 16-token pages a block-table row addresses
-    int bt_cols, page_shift;  // block-table columns; page_size = 16 << page_shift
+    int bt_cols, page_shift;  // block-table columns; the page code of virtual_page (page_size = 16 m)
     float log2_scale;
 };
 

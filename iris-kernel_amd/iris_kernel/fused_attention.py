@@ -46,7 +46,8 @@ DECODE_PAGE_KERNEL = 0x100
 DECODE_VALU_TILE = 0x200
 # The any-shape kernel (IRIS_DECODE_ANY_KERNEL): every head_dim that is a
 # multiple of 32 up to 512, every page size.  The plan picks it by itself for
-# such head dims; page sizes other than 16 << k must ask for it.
+# such head dims; page sizes that are not a multiple of 16 up to 256 must ask
+# for it.
 DECODE_ANY_KERNEL = 0x400
 
 
@@ -56,8 +57,9 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
     """(chunk_tiles, max_chunks, waves_per_block, workspace_bytes) from iris_decode_plan.
 
     ``max_pages`` counts 16-token pages: ceil(block_table columns * page_size / 16).
-    For page sizes other than 16 << k, or ``head_dim`` other than 64, 128 and
-    256, use ``int4_decode_plan``, which asks for the any-shape kernel."""
+    For page sizes that are not a multiple of 16 up to 256, or ``head_dim``
+    other than 64, 128 and 256, use ``int4_decode_plan``, which asks for the
+    any-shape kernel."""
     ct, mc, nw = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
     ws = ctypes.c_int64()
     status = _lib.lib().iris_decode_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages,
@@ -69,8 +71,9 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
 
 
 def _fast_page_size(page_size: int) -> bool:
-    """Page sizes the streaming, page and general kernels read: 16 << k, 16-256."""
-    return page_size in (16, 32, 64, 128, 256)
+    """Page sizes the streaming, MQA, page and general kernels read: 16 m
+    for m = 1..16 (a page is m consecutive 16-token pages)."""
+    return page_size % 16 == 0 and 16 <= page_size <= 256
 
 
 def int4_decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
@@ -79,7 +82,7 @@ def int4_decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: 
     """The decode plan for a cache of ``page_size``-token pages and a block
     table ``bt_cols`` columns wide: ``decode_plan`` over the tokens a row
     addresses, with the any-shape kernel asked for when the page size is not
-    16 << k."""
+    a multiple of 16 up to 256."""
     if not _fast_page_size(page_size):
         waves_per_block = (max(waves_per_block, 0) & 0xFF) | DECODE_ANY_KERNEL
     return decode_plan(batch, num_q_heads, num_kv_heads, head_dim, -(-bt_cols * page_size // 16), total_tokens,

@@ -62,8 +62,9 @@ def test_decode_rejects_unsupported_shapes_before_launch():
                                                     null, 0, a["B"], a["Hq"], a["Hkv"], a["D"], a["P"],
                                                     a["NP"], a["maxP"], ctypes.c_float(0.1), a["ct"],
                                                     a["mc"], a["nw"], null)
-    assert call(P=48) == 1          # page_size must be 16 << k (without the any-shape bit)
+    assert call(P=24) == 1          # page_size must be a multiple of 16 up to 256 (without the any-shape bit)
     assert call(P=8) == 1
+    assert call(P=272) == 1
     assert call(P=512) == 1
     assert call(D=96) == 1          # head_dim in {64, 128, 256} (without the any-shape bit)
     assert call(D=512) == 1
@@ -255,14 +256,18 @@ def test_decode_plan_overrides_and_errors():
     for bad in (80, 544, 0):
         with pytest.raises(RuntimeError):
             decode_plan(2, 8, 2, bad, 64)
-    # page sizes other than 16 << k: int4_decode_plan asks for the any-shape kernel
+    # page sizes that are not a multiple of 16 up to 256: int4_decode_plan
+    # asks for the any-shape kernel; multiples of 16 (48, 80, ...) plan the
+    # fast kernels over 16-token pages
     from iris_kernel.fused_attention import int4_decode_plan
 
-    assert int4_decode_plan(2, 8, 2, 128, 48, 10)[2] == 4 | 0x400
+    assert int4_decode_plan(2, 8, 2, 128, 24, 10)[2] == 4 | 0x400
     assert int4_decode_plan(2, 8, 2, 128, 1, 1000)[2] == 4 | 0x400
+    assert int4_decode_plan(2, 8, 2, 128, 272, 10)[2] == 4 | 0x400
     assert int4_decode_plan(2, 8, 2, 128, 32, 10)[2] in (4, 16)
-    ct, mc, nw, ws = int4_decode_plan(3, 8, 2, 128, 48, 10, tokens_per_split=64)
-    assert ct * 32 * mc >= 10 * 48 and ct % 2 == 0
+    assert int4_decode_plan(2, 8, 2, 128, 48, 10)[2] in (1, 2, 3, 4, 16)
+    ct, mc, nw, ws = int4_decode_plan(3, 8, 2, 128, 8, 60, tokens_per_split=64)
+    assert ct * 32 * mc >= 60 * 8 and ct % 2 == 0 and nw & 0x400
 
 
 def any_workspace(batch, hq, d, max_chunks):

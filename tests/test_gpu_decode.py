@@ -478,6 +478,42 @@ def test_wider_scope_matches_eager(device, kernel, hq, hkv, d, page, lens, tps):
 # pages, a one-token sequence, steps with fewer tiles than waves), splits of
 # 1 to many chunks, fewer query heads than MFMA columns, pages of 16 << k
 # tokens, fp32 and fp16 outputs.
+# Pages of 16 m tokens with m not a power of two (48, 80, 144, 240): the
+# fast kernels read a page as m consecutive 16-token pages, looked up with
+# a division instead of a shift; each kernel choice, with and without
+# split-KV, against the eager attention.
+@pytest.mark.parametrize("kernel", ["auto", "wave16", "pages", "general"])
+@pytest.mark.parametrize("hq,hkv,d,page,lens,tps", [
+    (32, 8, 128, 48, [47, 48, 49, 1500, 3001], 0),
+    (32, 8, 128, 80, [100, 2000], 256),
+    (16, 1, 64, 144, [143, 145, 5000], 512),     # one kv head: the MQA kernel at 16 waves
+    (64, 8, 128, 240, [239, 4000], 0),           # 8 query heads per kv head
+    (16, 4, 128, 48, [900, 10, 2500], 1024),
+])
+def test_page_sizes_multiple_of_16_match_eager(device, kernel, hq, hkv, d, page, lens, tps):
+    from iris_kernel.fused_attention import int4_decode_plan
+    waves = {"auto": 0, "wave16": 16, "pages": 16 | DECODE_PAGE_KERNEL, "general": 4}[kernel]
+    log(f"decode: P={page} Hq={hq} Hkv={hkv} D={d} lens={lens} split={tps} kernel={kernel}")
+    g = torch.Generator().manual_seed(page * 3 + hq + len(lens) + tps)
+    B = len(lens)
+    cols = max(-(-n // page) for n in lens) + 1
+    num_pages = B * cols + 2
+    kd, vd, ks, vs = _quantized_pool(num_pages, page, hkv, d, g)
+    bt = torch.randperm(num_pages, generator=g)[: B * cols].view(B, cols).to(torch.int32)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    q = torch.randn(B, hq, d, generator=g).to(torch.float16)
+    plan = int4_decode_plan(B, hq, hkv, d, page, cols, sum(lens), max(lens), tps, waves)
+    assert not plan[2] & 0x400, plan  # a fast kernel, not the any-shape one
+    want = torch_eager_int4_paged_decode_attention(q, kd, vd, ks, vs, bt, sl, page_size=page,
+                                                   out_dtype=torch.float32)
+    out = torch.empty(q.shape, dtype=torch.float32, device=device)
+    fused_int4_paged_decode_attention(*to(device, q, kd, vd, ks, vs, bt, sl), out, page_size=page,
+                                      tokens_per_split=tps, waves_per_block=waves)
+    torch.cuda.synchronize(device)
+    e = assert_attention_close(out.cpu(), want, f"P={page} Hq={hq} Hkv={hkv} D={d} {kernel} plan={plan}")
+    log(f"decode: P={page} {kernel} plan {plan} max-abs err {e:.2e}")
+
+
 @pytest.mark.parametrize("hq,page,lens,tps", [
     (16, 16, [8192, 8192, 8192], 0),          # configuration 4's shape, plan's split
     (16, 16, [1, 17, 33, 511, 4097], 0),

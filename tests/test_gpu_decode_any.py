@@ -1,6 +1,6 @@
 """INT4 decode at the shapes only the any-shape kernel reads: head dims that
 are multiples of 32 other than 64, 128 and 256 (32 to 512), page sizes that
-are not 16 << k (one token a page, 8, 48), more than 16 query heads per kv
+are not multiples of 16 (one token a page, 8, 24, 40), more than 16 query heads per kv
 head on such shapes -- everything the eager path takes
 (torch_eager_attention.py:72, :93 of the reference) and its fused path
 refuses (fused_attention.py:390-403).  Checked against the checker's eager
@@ -64,7 +64,8 @@ def _check(device, q, cache, bt, sl, page, what, **kw):
     (8, 2, 128, 1, [1, 2, 63, 64, 65, 500]),      # one token a page
     (32, 8, 128, 8, [7, 8, 9, 1111]),             # 8-token pages
     (8, 2, 96, 48, [47, 48, 49, 2000]),           # 48-token pages
-    (16, 1, 64, 48, [300, 3000]),                 # MQA at 48-token pages
+    (16, 1, 64, 24, [300, 3000]),                 # MQA at 24-token pages
+    (8, 2, 128, 40, [39, 40, 41, 999]),           # 40-token pages
     (40, 2, 96, 48, [77, 1234]),                  # 20 query heads per kv head: two blocks
     (64, 2, 320, 1, [3, 260]),                    # 32 per kv head, head_dim 320, one token a page
 ])
