@@ -65,6 +65,7 @@
 
 #include "common.h"
 #include "decode_any.h"
+#include "decode_hd.h"
 #include "decode_mqa.h"
 #include "decode_pages.h"
 #include "decode_stream.h"
@@ -1449,6 +1450,11 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
         return kInvalidArgument;
     const int32_t sel = selection_of(waves_per_block);
     if (sel < 0) return kInvalidArgument;
+    // head_dim 96, 160, 192 and 224: the MFMA kernel of decode_hd.hip
+    // (page sizes of 16 m tokens; the others ask for the any-shape kernel).
+    if (sel == 0 && hd_supported(head_dim))
+        return hd_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, max_tokens, tokens_per_split,
+                       out_chunk_tiles, out_max_chunks, out_waves, out_workspace_bytes);
     if (sel == kAnyKernel || !fast_head_dim(head_dim)) {
         const int st = any_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages * kPageSize, total_tokens,
                                 max_tokens, tokens_per_split, out_chunk_tiles, out_max_chunks, out_workspace_bytes);
@@ -1548,7 +1554,8 @@ extern "C" int iris_int4_paged_decode_attention(
     // per row (the count the plan was made with); they take the page code
     // log2(m) for a power of two, else -m (virtual_page in common.h).
     if (page_size < kPageSize || page_size > 16 * kPageSize || page_size % kPageSize != 0 || batch <= 0 ||
-        num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || !fast_head_dim(head_dim) || max_pages <= 0 ||
+        num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
+        !(fast_head_dim(head_dim) || hd_supported(head_dim)) || max_pages <= 0 ||
         max_pages * (page_size / kPageSize) > 0x3FFFFFFF)
         return kInvalidArgument;
     const int page_mul = (int)(page_size / kPageSize);
@@ -1556,6 +1563,12 @@ extern "C" int iris_int4_paged_decode_attention(
     const int64_t bt_cols = max_pages;
     max_pages *= page_mul;
     const int32_t waves = waves_of(waves_per_block);
+    if (hd_supported(head_dim)) {
+        if (sel != 0) return kInvalidArgument;
+        return hd_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
+                         workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, max_pages,
+                         bt_cols, shift, softmax_scale, chunk_tiles, max_chunks, waves, stream);
+    }
     if (waves == mqa_waves() && mqa_allowed(waves_per_block) &&
         mqa_supported(num_q_heads, num_kv_heads, head_dim) && chunk_tiles > 0)
         return mqa_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,

@@ -32,6 +32,7 @@ SOURCES = {
     "decode_stream.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=10"],
     "decode_mqa.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
     "decode_any.hip": [],
+    "decode_hd.hip": [],
     "decode_fp16.hip": [],
     "decode_fp16_stream.hip": [],
     "kv_fp16.hip": ["-ffp-contract=off"],

@@ -66,8 +66,20 @@ def test_decode_rejects_unsupported_shapes_before_launch():
     assert call(P=8) == 1
     assert call(P=272) == 1
     assert call(P=512) == 1
-    assert call(D=96) == 1          # head_dim in {64, 128, 256} (without the any-shape bit)
-    assert call(D=512) == 1
+    assert call(D=512) == 1         # head_dim in {64, 96, 128, 160, 192, 224, 256} (without the any-shape bit)
+    assert call(D=80) == 1
+    # head_dim 96, 160, 192, 224: their own kernel, 12 waves at 96, 8 above
+    assert call(D=96, nw=12, ct=12, mc=1) == 2              # valid: it gets as far as the launch
+    assert call(D=224, nw=8, ct=8, mc=1) == 2
+    assert call(D=96, P=48, nw=12, ct=12, mc=1) == 2        # pages of 16 m tokens
+    assert call(D=96) == 1                                  # its wave count only (4 asked)
+    assert call(D=160, nw=12, ct=12, mc=1) == 1
+    assert call(D=96, nw=12, ct=121, mc=1) == 1             # a chunk holds at most 120 tiles at 12 waves
+    assert call(D=192, nw=8, ct=129, mc=1) == 1             # ... 128 at 8
+    assert call(D=96, nw=12, ct=1, mc=1) == 1               # chunks do not cover max_pages
+    assert call(D=96, nw=12, ct=2, mc=2) == 3               # two chunks need a workspace
+    assert call(D=96, nw=12 | 0x100, ct=12, mc=1) == 1      # no selection bit but the any-shape one
+    assert call(D=96, P=24, nw=12, ct=12, mc=1) == 1        # page sizes of 16 m tokens only
     # the any-shape kernel: any page size, head_dim a multiple of 32 up to 512
     any_ = 4 | 0x400
     assert call(P=48, D=96, nw=any_, ct=6, mc=1) == 2      # valid: it gets as far as the launch
@@ -248,11 +260,23 @@ def test_decode_plan_overrides_and_errors():
     assert ws == pages_workspace(2, 8, 128, 16)
     # ... and falls back to the general kernel where it has no layout (Hkv=3)
     assert decode_plan(2, 9, 3, 128, 64, waves_per_block=16)[2] == 4
-    # head dims other than 64 / 128 / 256 plan the any-shape kernel by themselves
+    # head_dim 96, 160, 192, 224 plan their own kernel: chunks of whole steps
+    # of its waves (256 tokens -> 8 tiles -> 12 at 12 waves), the any-shape
+    # kernel's workspace layout
     ct, mc, nw, ws = decode_plan(2, 8, 2, 96, 64, tokens_per_split=256)
+    assert (ct, mc, nw) == (12, 3, 12), (ct, mc, nw)
+    assert ws == any_workspace(2, 8, 96, 3)
+    ct, mc, nw, ws = decode_plan(2, 40, 2, 224, 64, tokens_per_split=256)
+    assert (ct, mc, nw) == (8, 4, 8), (ct, mc, nw)
+    assert ws == any_workspace(2, 40, 224, 4)
+    assert decode_plan(1, 8, 8, 160, 64)[:3] == (8, 4, 8)   # 32 tiles over 8 units: a tile a wave
+    assert decode_plan(4, 32, 8, 192, 4096)[2] == 8
+    # ... and the any-shape kernel when asked; other head dims plan it by themselves
+    ct, mc, nw, ws = decode_plan(2, 8, 2, 96, 64, tokens_per_split=256, waves_per_block=0x400)
     assert (ct, mc, nw) == (8, 4, 4 | 0x400), (ct, mc, nw)
     assert ws == any_workspace(2, 8, 96, 4)
     assert decode_plan(2, 8, 2, 512, 64)[2] == 4 | 0x400
+    assert decode_plan(2, 8, 2, 32, 64)[2] == 4 | 0x400
     for bad in (80, 544, 0):
         with pytest.raises(RuntimeError):
             decode_plan(2, 8, 2, bad, 64)

@@ -1,13 +1,14 @@
-"""INT4 decode at the shapes only the any-shape kernel reads: head dims that
-are multiples of 32 other than 64, 128 and 256 (32 to 512), page sizes that
-are not multiples of 16 (one token a page, 8, 24, 40), more than 16 query heads per kv
-head on such shapes -- everything the eager path takes
-(torch_eager_attention.py:72, :93 of the reference) and its fused path
-refuses (fused_attention.py:390-403).  Checked against the checker's eager
-attention (fp32 values within helpers.ATOL; fp16 outputs within one ulp),
-with one chunk a sequence and with split-KV, on caches written by the
-package's own append; plus the any-shape kernel forced at the fast kernels'
-shapes, where it must agree with them."""
+"""INT4 decode on the any-shape kernel: head dims that are multiples of 32
+(32 to 512; 96, 160, 192 and 224 have an MFMA kernel of their own, so the
+kernel is asked for here), page sizes that are not multiples of 16 (one
+token a page, 8, 24, 40), more than 16 query heads per kv head on such
+shapes -- everything the eager path takes (torch_eager_attention.py:72, :93
+of the reference) and its fused path refuses (fused_attention.py:390-403).
+Checked against the checker's eager attention (fp32 values within
+helpers.ATOL; fp16 outputs within one ulp), with one chunk a sequence and
+with split-KV, on caches written by the package's own append; plus the
+any-shape kernel forced at the fast kernels' shapes, where it must agree
+with them."""
 import pytest
 import torch
 
@@ -72,10 +73,11 @@ def _check(device, q, cache, bt, sl, page, what, **kw):
 def test_any_shape_matches_eager(device, hq, hkv, d, page, lens, tps):
     log(f"decode any: Hq={hq} Hkv={hkv} D={d} P={page} lens={lens} split={tps}")
     q, cache, bt, sl = _case(hq, hkv, d, page, lens, hq * 7 + d + page + tps)
-    plan = int4_decode_plan(len(lens), hq, hkv, d, page, bt.shape[1], int(sl.sum()), int(sl.max()), tps)
+    plan = int4_decode_plan(len(lens), hq, hkv, d, page, bt.shape[1], int(sl.sum()), int(sl.max()), tps,
+                            DECODE_ANY_KERNEL)
     assert plan[2] & DECODE_ANY_KERNEL, plan
     e32, e16 = _check(device, q, cache, bt, sl, page, f"Hq={hq} Hkv={hkv} D={d} P={page} split={tps}",
-                      tokens_per_split=tps)
+                      tokens_per_split=tps, waves_per_block=DECODE_ANY_KERNEL)
     log(f"decode any: max-abs err fp32 {e32:.2e} fp16 {e16:.2e} (plan {plan})")
 
 
@@ -109,7 +111,7 @@ def test_any_shape_reads_what_the_append_writes(device, d, page):
     cpu = tuple(t.cpu() for t in cache)
     for tps in (0, 256):
         e32, e16 = _check(device, q, cpu, bt, sl, page, f"append-written D={d} P={page} split={tps}",
-                          tokens_per_split=tps)
+                          tokens_per_split=tps, waves_per_block=DECODE_ANY_KERNEL)
         log(f"decode any: append-written D={d} P={page} split={tps}: fp32 {e32:.2e} fp16 {e16:.2e}")
 
 
@@ -133,14 +135,15 @@ def test_any_kernel_forced_at_fast_shapes(device, cfg):
 
 def test_positional_handle_at_any_shape(device):
     # The sync-free positional handle plans for the widest batch the block
-    # table admits, at a 48-token page and head_dim 96.
-    q, cache, bt, sl = _case(8, 2, 96, 48, [40, 900], 5)
-    want = torch_eager_int4_paged_decode_attention(q, *cache, bt, sl, page_size=48, out_dtype=torch.float32)
+    # table admits, at a 24-token page and head_dim 96.
+    q, cache, bt, sl = _case(8, 2, 96, 24, [40, 900], 5)
+    assert int4_decode_plan(2, 8, 2, 96, 24, bt.shape[1])[2] & DECODE_ANY_KERNEL
+    want = torch_eager_int4_paged_decode_attention(q, *cache, bt, sl, page_size=24, out_dtype=torch.float32)
     gq, gbt, gsl = to(device, q, bt, sl)
     out = torch.empty(q.shape, dtype=torch.float32, device=device)
-    _int4_paged_decode_attention(gq, *to(device, *cache), gbt, gsl, out, 96, 48)
+    _int4_paged_decode_attention(gq, *to(device, *cache), gbt, gsl, out, 96, 24)
     torch.cuda.synchronize(device)
-    assert_attention_close(out, want, "positional handle D=96 P=48")
+    assert_attention_close(out, want, "positional handle D=96 P=24")
 
 
 def test_hip_graph_replay_at_any_shape(device):

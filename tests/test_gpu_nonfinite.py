@@ -15,8 +15,8 @@ the codes' +8 offset by a second sum, give NaN: both are non-finite.)
 Each case is run on the plan's own choice, on each INT4 kernel forced (the
 streaming kernel at its shapes (4 and 8 query heads per kv head), the MQA
 kernel at its shape, the page kernel,
-the general kernel and its VALU tile, the any-shape kernel, which a head_dim
-of 96 selects by itself), with one chunk a sequence and with
+the general kernel and its VALU tile, the kernel of head_dim 96 to 224, the
+any-shape kernel), with one chunk a sequence and with
 split-KV, and on a cache the package's own append wrote from an infinite key
 and value.  The FP16-cache decode gets the same check with NaN / Inf cache
 values."""
@@ -54,7 +54,9 @@ KERNELS = [
     ("mqa-valu", 16, 1, 64, 4 | DECODE_VALU_TILE),
     ("gqa-any", 32, 8, 128, DECODE_ANY_KERNEL),
     ("mqa-any", 16, 1, 64, DECODE_ANY_KERNEL),
-    ("d96-any", 8, 2, 96, 0),
+    ("d96-hd", 8, 2, 96, 0),
+    ("d224-hd", 12, 3, 224, 0),
+    ("d96-any", 8, 2, 96, DECODE_ANY_KERNEL),
 ]
 
 # (name, what is poisoned): sequence b, token t < L_b, kv head, scale group.

@@ -12,7 +12,7 @@ import pytest
 from isa_hazards import kernel_lines, kernel_symbols, split_kv_order
 
 DECODE_SOURCES = ["decode.hip", "decode_pages.hip", "decode_stream.hip", "decode_mqa.hip", "decode_fp16.hip",
-                  "decode_fp16_stream.hip", "decode_any.hip"]
+                  "decode_fp16_stream.hip", "decode_any.hip", "decode_hd.hip"]
 
 
 @pytest.mark.parametrize("src", DECODE_SOURCES)
