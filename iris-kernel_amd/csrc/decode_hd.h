@@ -23,7 +23,8 @@ IRIS_INTERNAL int hd_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_hea
                           int64_t max_pages, int64_t max_tokens, int32_t tokens_per_split, int32_t* out_chunk_tiles,
                           int32_t* out_max_chunks, int32_t* out_waves, int64_t* out_workspace_bytes);
 
-// Launch: batch x num_kv_heads x ceil(g / 16) x max_chunks workgroups of
+// Launch: num_kv_heads x (batch x ceil(g / 16) x max_chunks, rounded up to 8)
+// workgroups (the kv heads of one unit on one XCD) of
 // `waves` (= hd_waves) waves; max_pages counts 16-token pages, page_code is
 // virtual_page's (common.h).
 IRIS_INTERNAL int hd_launch(const void* query, const void* k_data, const void* v_data, const void* k_scale,

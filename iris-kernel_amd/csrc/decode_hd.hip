@@ -49,7 +49,7 @@ namespace iris {
 namespace hd {
 
 constexpr int kTile = 32;
-constexpr int kMaxChunkTiles = 128;  // a chunk holds at most 128 / W tiles a wave (two page ids each)
+constexpr int kMaxTilesPerWave = 32;  // a wave's page ids (two a tile) fill its 64 lanes
 constexpr int kMaxChunks = 64;
 constexpr int kMergeBatch = 8;
 constexpr int kHeads = 16;  // query heads of a workgroup (a block of its kv head's)
@@ -60,9 +60,11 @@ typedef int int2v_t __attribute__((ext_vector_type(2)));
 template <int G_>
 struct Geo {
     static constexpr int G = G_, D = 32 * G_, HB = 16 * G_;  // groups, head_dim, code bytes of a head row
-    static constexpr int W = G_ <= 3 ? 12 : 8;               // waves a workgroup
-    static constexpr int NK = (32 * G_ + 63) / 64;           // 16-byte loads a tensor a tile
-    static constexpr int KA = 1024 * NK;                     // code area of a slot, per tensor
+    // waves a workgroup and LDS slots a wave (R - 1 tiles in flight while one is computed)
+    static constexpr int W = G_ <= 3 ? 12 : 8;
+    static constexpr int R = G_ <= 5 ? 3 : 2;
+    static constexpr int NK = (32 * G_ + 63) / 64;  // 16-byte loads a tensor a tile
+    static constexpr int KA = 512 * G_;             // code area of a slot, per tensor (32 G pieces)
     static constexpr int SD = G_ / 2 + 1;                    // scale dwords a token needs (at most)
     static constexpr int SP = SD <= 2 ? 2 : 4;               // scale dwords a token occupies in LDS
     static constexpr int NS = 32 * SP / 64;                  // 4-byte loads a scale tensor a tile
@@ -70,12 +72,12 @@ struct Geo {
     // Slot: [K pieces 32 G x 16 B (area KA)][V pieces (KA)][K scales 32 x SP dwords][V scales]
     static constexpr int K_OFF = 0, V_OFF = KA, KS_OFF = 2 * KA, VS_OFF = 2 * KA + 128 * SP;
     static constexpr int SLOT = 2 * KA + 256 * SP;
-    static constexpr int RING_BYTES = W * 2 * SLOT;
+    static constexpr int RING_BYTES = W * R * SLOT;
     // Epilogue over the ring: per wave [m 16][l 16][o 16 heads x (D + 1)] fp32.
     static constexpr int EPI_ROW = D + 1, EPI_FLOATS = 32 + kHeads * EPI_ROW;
     static constexpr int CTL_OFF = W * EPI_FLOATS * 4;
     static constexpr int LDS_BYTES = RING_BYTES > CTL_OFF + 16 ? RING_BYTES : CTL_OFF + 16;
-    static_assert(2 * kMaxChunkTiles / W <= 64, "a wave's page ids fit its lanes");
+    static_assert(R >= 2 && R <= 4, "ring depth");
     static_assert(NA <= SP && SD <= SP, "scale dwords of a token");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS of a CU");
 };
@@ -94,6 +96,7 @@ struct Args {
     float* part_ml;      // [B][max_chunks][Hq][2] (m, l), base-2 logits
     int out_f32;
     int n_q_heads, n_kv_heads, group, q_blocks;
+    int n_units;  // batch x q_blocks x max_chunks
     int max_chunks, chunk_tiles;
     int max_pages;            // 16-token pages a block-table row addresses
     int bt_cols, page_code;   // block-table columns; the page code of virtual_page (page_size = 16 m)
@@ -312,16 +315,23 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     const int n = lane & 15;   // MFMA row (A) or column (B, C): token or query head
     const int jq = lane >> 4;  // MFMA k-chunk (A, B) or row quad (C)
 
-    // ---- (sequence b, kv head, query block, chunk), chunks fastest.  The
-    // divisions run on the VALU; readfirstlane keeps the results, and all
-    // that derives from them (the loop bounds among it), scalar.
-    int rest = blockIdx.x;
-    const int chunk = __builtin_amdgcn_readfirstlane(rest % a.max_chunks);
-    rest = __builtin_amdgcn_readfirstlane(rest / a.max_chunks);
+    // ---- (kv head, unit = (sequence b, query block, chunk)).  Workgroups
+    // are dispatched to the 8 XCDs in turn (workgroup i to XCD i % 8), and a
+    // kv head's rows are only 16 G of each token's Hkv 16 G bytes: the kv
+    // heads of one unit run on one XCD, one after another (k = i / 8, unit
+    // (k / Hkv) 8 + i % 8, kv head k % Hkv), so the cache lines they share
+    // are fetched into one L2.  The grid is padded to whole groups of 8
+    // units; padding workgroups return at once.  The divisions run on the
+    // VALU; readfirstlane keeps the results, and all that derives from them
+    // (the loop bounds among it), scalar.
+    const int k_x = blockIdx.x >> 3;
+    const int kvh = __builtin_amdgcn_readfirstlane(k_x % a.n_kv_heads);
+    const int unit = __builtin_amdgcn_readfirstlane((k_x / a.n_kv_heads) * 8 + (blockIdx.x & 7));
+    if (unit >= a.n_units) return;
+    const int chunk = __builtin_amdgcn_readfirstlane(unit % a.max_chunks);
+    const int rest = __builtin_amdgcn_readfirstlane(unit / a.max_chunks);
     const int qb = __builtin_amdgcn_readfirstlane(rest % a.q_blocks);
-    rest = __builtin_amdgcn_readfirstlane(rest / a.q_blocks);
-    const int kvh = __builtin_amdgcn_readfirstlane(rest % a.n_kv_heads);
-    const int b = __builtin_amdgcn_readfirstlane(rest / a.n_kv_heads);
+    const int b = __builtin_amdgcn_readfirstlane(rest / a.q_blocks);
     const int t_begin = chunk * a.chunk_tiles;
     const int p0 = 2 * t_begin;  // first 16-token page of the chunk
     const int32_t* bt = a.block_table + (int64_t)b * a.bt_cols;
@@ -332,9 +342,8 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     // ---- this wave's page ids (lane l < 2 chunk_tiles / W: chunk page
     // 2 (W (l >> 1) + wave) + (l & 1), i.e. page l & 1 of its tile l >> 1,
     // clamped into the table row), q and the length, in flight together
-    int my_pid = 0;
-    if (lane < 2 * (kMaxChunkTiles / W))
-        my_pid = virtual_page(bt, min(p0 + 2 * (W * (lane >> 1) + wave) + (lane & 1), a.max_pages - 1), a.page_code);
+    const int my_pid =
+        virtual_page(bt, min(p0 + 2 * (W * (lane >> 1) + wave) + (lane & 1), a.max_pages - 1), a.page_code);
     // q as the QK B operand: lane (head n, k-chunk jq) holds dims 32 g + 8 jq
     // .. + 7 of head n (zero for columns past the block's heads)
     const bool col_valid = n < nh;
@@ -389,10 +398,10 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
         sc_ok[i] = 2 * j < G + sh;  // the dword holds some of the kv head's halves
         sc_off[i] = (uint32_t)((h0 - sh) * 2 + 4 * j);
     }
-    uint8_t* const ring = smem + wave * 2 * SLOT;
+    uint8_t* const ring = smem + wave * L::R * SLOT;
     const int n_my = n_ct > wave ? (n_ct - wave + W - 1) / W : 0;
-    auto issue = [&](int s) __attribute__((always_inline)) {
-        uint8_t* const dst = ring + (s & 1) * SLOT;
+    auto issue = [&](int s, int slot) __attribute__((always_inline)) {
+        uint8_t* const dst = ring + slot * SLOT;
         const int t = W * s + wave;  // chunk-relative tile
         const int pa = __builtin_amdgcn_readlane(my_pid, 2 * s);
         const int pb = 2 * t + 1 > jlim ? pa : __builtin_amdgcn_readlane(my_pid, 2 * s + 1);
@@ -425,7 +434,9 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
             }
         }
     };
-    if (n_my > 0) issue(0);
+#pragma unroll
+    for (int s = 0; s < L::R - 1; ++s)
+        if (s < n_my) issue(s, s);
 
     // ---- q operands (in the order of k_operand; high-nibble dims / 16) and
     // the accumulator start that removes the +8 of the K codes: C row (token)
@@ -587,22 +598,33 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
         }
     };
 
-    // ---- the pipeline, per wave (no workgroup barrier): tile s + 1 is
-    // issued into the other slot (whose reads, by tile s - 1, have
-    // returned), then tile s is computed once this wave's loads of it have
-    // landed (vmcnt counts in order; every load instruction of a tile has a
-    // lane that issues it, so a tile is always JOBS of them).
+    // ---- the pipeline, per wave (no workgroup barrier): tile s is computed
+    // once this wave's loads of it have landed (vmcnt counts in order; every
+    // load instruction of a tile has a lane that issues it, so a tile is
+    // always JOBS of them), with tiles s + 1 .. s + R - 1 in flight; slot
+    // (s - 1) % R, whose reads by tile s - 1 have returned, receives tile
+    // s + R - 1 first.
+    constexpr int R = L::R;
     constexpr int JOBS = 2 * NK + 2 * NS;
-    static_assert(JOBS < 64, "vmcnt range");
+    static_assert((R - 1) * JOBS < 64, "vmcnt range");
     const uint32_t ring_addr = lds_addr(ring);
+    int slot_c = 0;          // slot of tile s
+    int slot_i = R - 1;      // slot of tile s + R - 1
     for (int s = 0; s < n_my; ++s) {
-        if (s + 1 < n_my) {
-            issue(s + 1);
+        const int ahead = min(n_my - 1 - s, R - 1);  // tiles in flight behind tile s
+        if (ahead == R - 1) {
+            issue(s + R - 1, slot_i);
+            wait_vmcnt<(R - 1) * JOBS>();
+        } else if (R > 3 && ahead == 2) {
+            wait_vmcnt<2 * JOBS>();
+        } else if (R > 2 && ahead == 1) {
             wait_vmcnt<JOBS>();
         } else {
             wait_vmcnt<0>();
         }
-        compute(t_begin + W * s + wave, ring_addr + (uint32_t)((s & 1) * SLOT));
+        compute(t_begin + W * s + wave, ring_addr + (uint32_t)(slot_c * SLOT));
+        slot_c = slot_c == R - 1 ? 0 : slot_c + 1;
+        slot_i = slot_i == R - 1 ? 0 : slot_i + 1;
     }
     wait_vmcnt<0>();
     __syncthreads();
@@ -734,11 +756,17 @@ bool hd_supported(int64_t head_dim) {
     return head_dim == 96 || head_dim == 160 || head_dim == 192 || head_dim == 224;
 }
 
-int hd_waves(int64_t head_dim) { return head_dim <= 96 ? 12 : 8; }
+int hd_waves(int64_t head_dim) {
+    switch (head_dim) {
+        case 96: return hd::Geo<3>::W;
+        case 160: return hd::Geo<5>::W;
+        case 192: return hd::Geo<6>::W;
+        default: return hd::Geo<7>::W;
+    }
+}
 
-// Tiles a chunk may hold: a wave's page ids (two a tile) sit in
-// 2 (kMaxChunkTiles / W) lanes.
-static int64_t hd_max_chunk_tiles(int W) { return hd::kMaxChunkTiles / W * W; }
+// Tiles a chunk may hold: a wave's page ids, two a tile, fill its 64 lanes.
+static int64_t hd_max_chunk_tiles(int W) { return (int64_t)hd::kMaxTilesPerWave * W; }
 
 static int64_t hd_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t max_chunks) {
     const int64_t rows = batch * max_chunks * num_q_heads;
@@ -815,7 +843,8 @@ int hd_launch(const void* query, const void* k_data, const void* v_data, const v
     const int64_t g = num_q_heads / num_kv_heads;
     const int64_t q_blocks = (g + hd::kHeads - 1) / hd::kHeads;
     if (max_chunks > 1 && num_kv_heads * q_blocks > kCountersPerSeq) return kInvalidArgument;
-    const int64_t nblocks = batch * num_kv_heads * q_blocks * (int64_t)max_chunks;
+    const int64_t units = batch * q_blocks * (int64_t)max_chunks;
+    const int64_t nblocks = (units + 7) / 8 * 8 * num_kv_heads;  // whole groups of 8 units (XCD order)
     if (nblocks > 0x7FFFFFFF || num_q_heads > 0x7FFFFFFF) return kInvalidArgument;
     hd::Args a;
     a.q = (const half_t*)query;
@@ -831,6 +860,7 @@ int hd_launch(const void* query, const void* k_data, const void* v_data, const v
     a.n_kv_heads = (int)num_kv_heads;
     a.group = (int)g;
     a.q_blocks = (int)q_blocks;
+    a.n_units = (int)units;
     a.max_chunks = max_chunks;
     a.chunk_tiles = chunk_tiles;
     a.max_pages = (int)max_pages;
