@@ -124,9 +124,11 @@ int iris_quantize_pack_int4(const void *x, void *packed, void *scales, int64_t n
  * unknown; max_pages (columns of block_table) bounds them.
  * tokens_per_split > 0 and waves_per_block > 0 override the heuristic:
  * its low 8 bits ask for a wave count (16: a page-streaming kernel; 1-4:
- * the general kernel), and one of the selection bits below may be or-ed
- * in.  out_waves carries the wave count and the selection bit into the
- * launch, so a plan and its launch always run the same kernel.
+ * the general kernel; head_dim 96, 160, 192 and 224 have a kernel of their
+ * own whose wave count, 12 or 8, the plan sets), and one of the selection
+ * bits below may be or-ed in.  out_waves carries the wave count and the
+ * selection bit into the launch, so a plan and its launch always run the
+ * same kernel.
  * max_pages counts 16-token pages: ceil(block_table columns * page_size /
  * 16), the tokens a row addresses.  head_dim any multiple of 32 up to 512;
  * any num_q_heads / num_kv_heads.
@@ -143,7 +145,8 @@ int iris_quantize_pack_int4(const void *x, void *packed, void *scales, int64_t n
 /* IRIS_DECODE_ANY_KERNEL: the any-shape kernel, which takes every head_dim
  * that is a multiple of 32 up to 512 and every page size, with fp32
  * dequantisation as the eager path does it.  iris_decode_plan sets it by
- * itself for head dims other than 64, 128 and 256; a caller whose page size
+ * itself for head dims other than 64, 96, 128, 160, 192, 224 and 256 (it
+ * may be asked for at those too); a caller whose page size
  * is not a multiple of 16 up to 256 must ask for it (the plan is not told
  * the page size), and iris_int4_paged_decode_attention refuses such a page
  * size without it.  At most one selection bit may be set. */

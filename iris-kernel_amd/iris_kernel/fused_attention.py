@@ -46,8 +46,9 @@ DECODE_PAGE_KERNEL = 0x100
 DECODE_VALU_TILE = 0x200
 # The any-shape kernel (IRIS_DECODE_ANY_KERNEL): every head_dim that is a
 # multiple of 32 up to 512, every page size.  The plan picks it by itself for
-# such head dims; page sizes that are not a multiple of 16 up to 256 must ask
-# for it.
+# head dims other than 64, 96, 128, 160, 192, 224 and 256 (96-224 have an
+# MFMA kernel of their own); page sizes that are not a multiple of 16 up to
+# 256 must ask for it.
 DECODE_ANY_KERNEL = 0x400
 
 
@@ -57,9 +58,8 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
     """(chunk_tiles, max_chunks, waves_per_block, workspace_bytes) from iris_decode_plan.
 
     ``max_pages`` counts 16-token pages: ceil(block_table columns * page_size / 16).
-    For page sizes that are not a multiple of 16 up to 256, or ``head_dim``
-    other than 64, 128 and 256, use ``int4_decode_plan``, which asks for the
-    any-shape kernel."""
+    For page sizes that are not a multiple of 16 up to 256 use
+    ``int4_decode_plan``, which asks for the any-shape kernel."""
     ct, mc, nw = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
     ws = ctypes.c_int64()
     status = _lib.lib().iris_decode_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages,

@@ -74,8 +74,9 @@ def test_decode_rejects_unsupported_shapes_before_launch():
     assert call(D=96, P=48, nw=12, ct=12, mc=1) == 2        # pages of 16 m tokens
     assert call(D=96) == 1                                  # its wave count only (4 asked)
     assert call(D=160, nw=12, ct=12, mc=1) == 1
-    assert call(D=96, nw=12, ct=121, mc=1) == 1             # a chunk holds at most 120 tiles at 12 waves
-    assert call(D=192, nw=8, ct=129, mc=1) == 1             # ... 128 at 8
+    assert call(D=96, nw=12, ct=385, mc=1) == 1             # a chunk holds at most 32 tiles a wave: 384 at 12
+    assert call(D=192, nw=8, ct=257, mc=1) == 1             # ... 256 at 8
+    assert call(D=192, nw=8, ct=256, mc=1) == 2
     assert call(D=96, nw=12, ct=1, mc=1) == 1               # chunks do not cover max_pages
     assert call(D=96, nw=12, ct=2, mc=2) == 3               # two chunks need a workspace
     assert call(D=96, nw=12 | 0x100, ct=12, mc=1) == 1      # no selection bit but the any-shape one
