@@ -248,10 +248,13 @@ int iris_int4_paged_decode_attention_noalloc(const void *query, const void *k_da
  * block_table admits stands in); tokens_per_split > 0 steers the chunk size.
  * Two kernels: a negative out_chunk_pages (chunks of -out_chunk_pages <= 128
  * pages, at most 16 a sequence) selects the page-streaming kernel (head_dim
- * 128 with 4 or 8 kv heads, head_dim 64 with 8 or 16, batches of similar
- * lengths: 4 * total_tokens >= 3 * batch * max_tokens); a positive one the
- * per-kv-head kernel (at most 256 pages a chunk, at most 512 chunks per
- * (sequence, kv head)).
+ * 128 with 4 or 8 kv heads, head_dim 64 with 8 or 16; the plan takes it for
+ * batches of similar lengths, 4 * total_tokens >= 3 * batch * max_tokens,
+ * of at least 8 sequences and 64 MB of K/V); a positive one the per-kv-head
+ * kernel (at most 256 pages a chunk, at most 512 chunks per (sequence, kv
+ * head)).  tokens_per_split < 0 (no reference counterpart; for A/B runs and
+ * tests) asks for the page-streaming kernel with chunks of -tokens_per_split
+ * tokens; unsupported shapes and chunks past 128 pages give status 1.
  */
 int iris_fp16_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                           int64_t max_pages, int64_t total_tokens, int64_t max_tokens,

@@ -410,9 +410,10 @@ using namespace iris;
 
 // Split plan of the FP16 decode: pages per chunk, chunks per sequence and
 // workspace bytes.  The page-streaming kernel (decode_fp16_stream.hip) takes
-// its shapes for batches of similar lengths (unknown lengths count as the
-// widest batch), with about one workgroup of all kv heads a CU; its plan has
-// a negative chunk_pages.  Ragged batches and the other shapes get the
+// its shapes for batches of similar lengths with enough work (at least 8
+// sequences and 64 MB of K/V, fp16_stream_preferred; unknown lengths count as
+// the widest batch), with about one workgroup of all kv heads a CU; its plan
+// has a negative chunk_pages.  Ragged batches and the other shapes get the
 // per-kv-head kernel's plan: about 1024 workgroups (four per CU), at least 8
 // pages (two per wave) each; one chunk when the longest sequence fits.  Both
 // kernels' workspaces have the same size for the same chunk count.
@@ -426,10 +427,16 @@ extern "C" int iris_fp16_decode_plan(int64_t batch, int64_t num_q_heads, int64_t
     const int64_t cap_tokens = max_pages * f16::kPage;
     if (max_tokens < 0 || max_tokens > cap_tokens) max_tokens = cap_tokens;
     if (total_tokens < 0) total_tokens = batch * max_tokens;
-    // (the page-streaming kernel's chunks are at most 16 a sequence: with
-    // ragged lengths the long sequences' chunks would outlast the rest;
-    // MI355X, configuration 3: 345 us against 235)
-    if (fp16_stream_supported(num_q_heads, num_kv_heads, head_dim) && 4 * total_tokens >= 3 * batch * max_tokens &&
+    // A negative tokens_per_split asks for the page-streaming kernel with
+    // chunks of -tokens_per_split tokens (A/B runs and tests).
+    const bool ask_stream = tokens_per_split < 0;
+    if (ask_stream) {
+        if (!fp16_stream_supported(num_q_heads, num_kv_heads, head_dim) || tokens_per_split == INT32_MIN)
+            return kInvalidArgument;
+        tokens_per_split = -tokens_per_split;
+    }
+    if (fp16_stream_supported(num_q_heads, num_kv_heads, head_dim) &&
+        (ask_stream || fp16_stream_preferred(batch, num_kv_heads, head_dim, total_tokens, max_tokens)) &&
         fp16_stream_plan(batch, max_pages, total_tokens, max_tokens, tokens_per_split, out_chunk_pages,
                          out_max_chunks) == kOk) {
         *out_workspace_bytes =
@@ -437,6 +444,7 @@ extern "C" int iris_fp16_decode_plan(int64_t batch, int64_t num_q_heads, int64_t
         *out_chunk_pages = -*out_chunk_pages;  // negative: the page-streaming kernel
         return kOk;
     }
+    if (ask_stream) return kInvalidArgument;  // chunks longer than 128 pages
     int64_t chunk_pages;
     if (tokens_per_split > 0) {
         chunk_pages = (tokens_per_split + f16::kPage - 1) / f16::kPage;

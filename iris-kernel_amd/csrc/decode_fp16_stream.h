@@ -13,6 +13,11 @@ namespace iris {
 // query heads per kv head.
 IRIS_INTERNAL bool fp16_stream_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim);
 
+// Whether the plan takes this kernel: batches of similar lengths, enough of
+// them to fill half the CUs, at least 64 MB of K/V.
+IRIS_INTERNAL bool fp16_stream_preferred(int64_t batch, int64_t num_kv_heads, int64_t head_dim,
+                                         int64_t total_tokens, int64_t max_tokens);
+
 // Chunks of at most 128 pages, at most 16 a sequence, covering the block table.
 IRIS_INTERNAL bool fp16_stream_plan_fits(int64_t max_pages, int32_t chunk_pages, int32_t max_chunks);
 

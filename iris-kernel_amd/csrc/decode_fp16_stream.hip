@@ -461,6 +461,20 @@ bool fp16_stream_supported(int64_t num_q_heads, int64_t num_kv_heads, int64_t he
     return false;
 }
 
+bool fp16_stream_preferred(int64_t batch, int64_t num_kv_heads, int64_t head_dim, int64_t total_tokens,
+                           int64_t max_tokens) {
+    // Batches of similar lengths (ragged ones leave the long sequences'
+    // chunks, at most 16 a sequence, running after the rest: configuration 3,
+    // 345 us against 235), enough sequences that their chunks fill half the
+    // CUs, and at least 64 MB of K/V.  MI355X, Hq=32, Hkv=8, D=128, against
+    // the per-kv-head kernel: B=1..4 at L=4096 (17-67 MB) 32.7-33.5 us
+    // against 18.6-29.8; B=4, L=16384 (64 workgroups) 100.8 against 72.4;
+    // B=8, L=4096 36.8 against 41.7; B=32 90.2 against 124.5.
+    if (4 * total_tokens < 3 * batch * max_tokens) return false;
+    if (batch * f16s::kMaxChunks < 128) return false;
+    return total_tokens * num_kv_heads * head_dim * 4 >= 64000000;
+}
+
 int64_t fp16_stream_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t head_dim, int64_t max_chunks) {
     const int64_t o = batch * max_chunks * num_q_heads * head_dim * 4;
     return counter_region_bytes(batch) + (o + 255) / 256 * 256 + batch * max_chunks * num_q_heads * 2 * 4;

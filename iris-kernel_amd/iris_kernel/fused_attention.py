@@ -378,7 +378,11 @@ def _int4_paged_decode_attention(query, k_data, v_data, k_scale, v_scale, block_
 def fp16_decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, max_pages: int,
                      total_tokens: int = -1, max_tokens: int = -1,
                      tokens_per_split: int = 0) -> tuple[int, int, int]:
-    """(chunk_pages, max_chunks, workspace_bytes) from iris_fp16_decode_plan."""
+    """(chunk_pages, max_chunks, workspace_bytes) from iris_fp16_decode_plan.
+
+    A negative ``chunk_pages`` is the page-streaming kernel's plan; a negative
+    ``tokens_per_split`` asks for that kernel (chunks of -tokens_per_split
+    tokens), as A/B runs and tests do."""
     cp, mc = ctypes.c_int32(), ctypes.c_int32()
     ws = ctypes.c_int64()
     status = _lib.lib().iris_fp16_decode_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages,

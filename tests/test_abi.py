@@ -146,6 +146,21 @@ def test_fp16_decode_plan():
     assert (cp, mc) == (4, 16)
     with pytest.raises(RuntimeError):
         fp16_decode_plan(2, 8, 2, 96, 64)
+    # the page-streaming kernel needs 8 sequences and 64 MB of K/V: one
+    # sequence of 4096 tokens (17 MB) or four (67 MB) get the other kernel,
+    # eight (134 MB) the page-streaming one
+    assert fp16_decode_plan(1, 32, 8, 128, 256, 4096, 4096)[0] > 0
+    assert fp16_decode_plan(4, 32, 8, 128, 256, 4 * 4096, 4096)[0] > 0
+    assert fp16_decode_plan(8, 32, 8, 128, 256, 8 * 4096, 4096)[0] < 0
+    assert fp16_decode_plan(8, 16, 8, 64, 256, 8 * 4096, 4096)[0] < 0      # 67 MB at head_dim 64
+    # ... unless asked for with a negative tokens_per_split (chunks of that many tokens)
+    cp, mc, ws = fp16_decode_plan(1, 32, 8, 128, 256, 4096, 4096, -1024)
+    assert (cp, mc) == (-64, 4) and ws > 0
+    assert fp16_decode_plan(1, 32, 8, 128, 256, 4096, 4096, -2048)[:2] == (-128, 2)   # 128-page chunks
+    for bad in ((1, 32, 2, 128, 256, 4096, 4096, -1024),     # 2 kv heads: no page-streaming layout
+                (1, 32, 8, 128, 256, 4096, 4096, -4096)):    # 256-page chunks
+        with pytest.raises(RuntimeError):
+            fp16_decode_plan(*bad)
 
 
 def general_kvw(B, Hq, Hkv, max_pages):

@@ -197,7 +197,10 @@ def test_fp16_page_streaming_kernel_matches_eager(device, hq, hkv, d, lens, tps,
     kc = torch.randn(NP, 16, hkv, d, generator=g).to(torch.float16)
     vc = torch.randn(NP, 16, hkv, d, generator=g).to(torch.float16)
     q = torch.randn(B, hq, d, generator=g).to(torch.float16)
-    plan = fp16_decode_plan(B, hq, hkv, d, maxp, -1, -1, tps)
+    # these small batches ask for the kernel (negative tokens_per_split;
+    # left to choose, the plan gives batches under 8 sequences or 64 MB the
+    # per-kv-head kernel)
+    plan = fp16_decode_plan(B, hq, hkv, d, maxp, -1, -1, -(tps or 1024))
     assert -128 <= plan[0] < 0 and plan[1] <= 16, plan  # the page-streaming kernel's plan
     assert fp16_decode_plan(B, hq, hkv, d, maxp, sum(lens), max(lens), tps)[0] > 0  # ragged: the other kernel
     want = torch_eager_fp16_paged_decode_attention(q, kc, vc, bt, sl, out_dtype=torch.float32)
