@@ -159,3 +159,24 @@ def test_hd_positional_handle_and_graph_replay(device):
         graph.replay()
         torch.cuda.synchronize(device)
         assert torch.equal(out, eager), f"replay {i} differs from the eager launch"
+
+
+def test_hd_workspace_shared_with_other_kernels(device):
+    # One caller workspace for split calls whose kernel alternates between
+    # the head-dim kernel (D=96, 3 kv heads) and the D=128 kernels, and whose
+    # batch grows and shrinks: every kernel keeps its counters at the same
+    # place per sequence, and the wrapper zeroes them only when the batch
+    # grows past the previous call's.
+    ws = torch.zeros(32 << 20, dtype=torch.uint8, device=device)
+    cases = {d: _case(12, 3, d, 16, [900, 1500, 64, 2000, 777, 1200, 33, 1800], 40 + d) for d in (96, 128)}
+    wants = {d: torch_eager_int4_paged_decode_attention(q, *cache, bt, sl, page_size=16, out_dtype=torch.float32)
+             for d, (q, cache, bt, sl) in cases.items()}
+    gpu = {d: (to(device, q, bt, sl), to(device, *cache)) for d, (q, cache, bt, sl) in cases.items()}
+    for d, n, waves in ((96, 8, 0), (128, 4, 4), (96, 8, 0), (128, 8, 16), (96, 2, 0), (128, 8, 4), (96, 5, 0)):
+        (gq, gbt, gsl), gcache = gpu[d]
+        out = torch.empty(n, 12, d, dtype=torch.float32, device=device)
+        fused_int4_paged_decode_attention(gq[:n], *gcache, gbt[:n], gsl[:n], out, tokens_per_split=256,
+                                          waves_per_block=waves, workspace=ws)
+        torch.cuda.synchronize(device)
+        assert_attention_close(out, wants[d][:n], f"D={d} batch {n} waves {waves}")
+

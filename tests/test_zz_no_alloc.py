@@ -56,8 +56,10 @@ def one_call(device, batch, max_pages, max_len, tokens_per_split, seed, hq=32, h
     cache = tuple(t.to(device) for t in cache)
     plan = decode_plan(batch, hq, hkv, d, max_pages, int(sl.sum()), int(sl.max()), tokens_per_split, waves)
     assert plan[1] > 1 and 0 < plan[3] <= SCRATCH_BYTES, plan
-    if waves:
+    if waves & 0xFF:
         assert plan[2] == waves, plan
+    elif waves:  # a selection bit alone: the plan names the wave count
+        assert plan[2] & ~0xFF == waves, plan
     log(f"no-alloc: batch={batch} hq={hq} hkv={hkv} d={d} max_len={max_len} plan={plan}")
     scale = d ** -0.5
     want = torch.empty(q.shape, dtype=torch.float16, device=device)
@@ -84,6 +86,19 @@ def test_noalloc_streaming_kernels_two_calls(device):
              waves=16)
     one_call(device, batch=6, max_pages=256, max_len=4096, tokens_per_split=0, seed=24, hq=16, hkv=1, d=64,
              waves=16)
+
+
+def test_noalloc_head_dim_and_any_shape_kernels_two_calls(device):
+    """The head_dim 96-224 kernel (the plan's choice at 96 and 224) and the
+    any-shape kernel (asked for, at 160), each larger call then smaller."""
+    one_call(device, batch=8, max_pages=128, max_len=2048, tokens_per_split=256, seed=31, hq=16, hkv=4, d=96)
+    one_call(device, batch=3, max_pages=64, max_len=1000, tokens_per_split=256, seed=32, hq=16, hkv=4, d=96)
+    one_call(device, batch=6, max_pages=96, max_len=1536, tokens_per_split=256, seed=33, hq=12, hkv=3, d=224)
+    one_call(device, batch=2, max_pages=32, max_len=500, tokens_per_split=128, seed=34, hq=12, hkv=3, d=224)
+    one_call(device, batch=5, max_pages=64, max_len=1024, tokens_per_split=256, seed=35, hq=8, hkv=2, d=160,
+             waves=0x400)
+    one_call(device, batch=2, max_pages=32, max_len=400, tokens_per_split=128, seed=36, hq=8, hkv=2, d=160,
+             waves=0x400)
 
 
 def test_noalloc_rejects_plan_beyond_scratch(device):
