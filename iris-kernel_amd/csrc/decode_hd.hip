@@ -13,12 +13,16 @@
 //
 // Streaming: a workgroup of W waves (12 at G = 3, 8 above) owns (sequence,
 // kv head, block of up to 16 of its query heads, chunk of 32-token tiles);
-// wave w streams tiles w, w + W, ... of the chunk through two LDS slots of
-// its own, with no workgroup barrier in the loop.  Per tile a wave
-// * issues the next tile's loads into its other slot, waits for this tile's
-//   (vmcnt) and computes it, reading the slot in two phases (K codes and
-//   scales before QK, V codes and scales before PV) so that only half of a
-//   tile's operands are live in registers at once;
+// the kv heads of one (sequence, query block, chunk) run on one XCD, one
+// after another, so the cache lines their rows share are fetched into one
+// L2.  Wave w streams tiles w, w + W, ... of the chunk through R LDS slots
+// of its own (three at G = 3 and 5, two above), with no workgroup barrier in
+// the loop.  Per tile a wave
+// * issues the loads of the tile R - 1 ahead into the slot the previous
+//   tile used, waits for this tile's (vmcnt) and computes it, reading the
+//   slot in two phases (K codes and scales before QK, V codes and scales
+//   before PV) so that only half of a tile's operands are live in registers
+//   at once;
 // * loads straight into LDS: the kv head's K and V rows of the tile's 32
 //   tokens (16 G bytes a token, one 16-byte piece a lane and load, the
 //   pieces token-major) and, per token, the aligned dwords that cover its
@@ -339,9 +343,9 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     const int nh = min(a.group - h_first, kHeads);  // query heads of the block
     const int hq0 = kvh * a.group + h_first;        // its first query head
 
-    // ---- this wave's page ids (lane l < 2 chunk_tiles / W: chunk page
-    // 2 (W (l >> 1) + wave) + (l & 1), i.e. page l & 1 of its tile l >> 1,
-    // clamped into the table row), q and the length, in flight together
+    // ---- this wave's page ids (lane l: chunk page 2 (W (l >> 1) + wave) +
+    // (l & 1), i.e. page l & 1 of its tile l >> 1, up to 32 tiles, clamped
+    // into the table row), q and the length, in flight together
     const int my_pid =
         virtual_page(bt, min(p0 + 2 * (W * (lane >> 1) + wave) + (lane & 1), a.max_pages - 1), a.page_code);
     // q as the QK B operand: lane (head n, k-chunk jq) holds dims 32 g + 8 jq
@@ -367,7 +371,7 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     // never read: a tile's second page past it is read as its first.
     const int jlim = min(last_lp - p0, 2 * n_ct - 1);
 
-    // ---- loads of this wave's tile s into its slot s & 1.
+    // ---- loads of this wave's tile s into slot `slot` of its ring.
     // Codes: piece p = 64 i + lane (p < 32 G) is token p / G, group p % G of
     // the tile, at 16 p in the tensor's area.
     // Scales: piece p = 64 i + lane is dword j = p % SP of token t = p / SP,
