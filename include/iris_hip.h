@@ -151,6 +151,15 @@ int iris_quantize_pack_int4(const void *x, void *packed, void *scales, int64_t n
  * the page size), and iris_int4_paged_decode_attention refuses such a page
  * size without it.  At most one selection bit may be set. */
 #define IRIS_DECODE_ANY_KERNEL 0x400
+/* IRIS_DECODE_TOKEN_PAGES: the MFMA kernel of head dims 96-224 in its
+ * token-page mode, which takes every page size (each token's page looked
+ * up through the table), at head_dim 64 to 224 in steps of 32 where
+ * head_dim / 32 x num_kv_heads is even.  Asked for at other shapes,
+ * iris_decode_plan returns the any-shape kernel's plan (out_waves then
+ * carries IRIS_DECODE_ANY_KERNEL).  It is the bit to ask for when the page
+ * size is not a multiple of 16 up to 256; it may be asked for at any page
+ * size. */
+#define IRIS_DECODE_TOKEN_PAGES 0x800
 int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                      int64_t max_pages, int64_t total_tokens, int64_t max_tokens,
                      int32_t tokens_per_split, int32_t waves_per_block, int32_t *out_chunk_tiles,
@@ -199,7 +208,8 @@ int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, i
  * (torch_eager_attention.py:72, :93; the reference's fused path takes
  * page_size 16, head_dim 64 or 128 and at most 16 query heads per kv head,
  * fused_attention.py:390-403).  Page sizes that are not a multiple of 16
- * up to 256 need a plan made with IRIS_DECODE_ANY_KERNEL.  max_pages is the number of
+ * up to 256 need a plan made with IRIS_DECODE_TOKEN_PAGES or
+ * IRIS_DECODE_ANY_KERNEL.  max_pages is the number of
  * block_table columns; plan with ceil(max_pages * page_size / 16).
  * Page ids and lengths are not
  * range-checked on the device (fused_attention.py:415-429 does that on the

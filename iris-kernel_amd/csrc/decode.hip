@@ -1383,12 +1383,17 @@ constexpr int32_t kWaveMask = 0xFF;
 constexpr int32_t kPageKernel = IRIS_DECODE_PAGE_KERNEL;
 constexpr int32_t kValuTile = IRIS_DECODE_VALU_TILE;
 constexpr int32_t kAnyKernel = IRIS_DECODE_ANY_KERNEL;
+constexpr int32_t kTokenPages = IRIS_DECODE_TOKEN_PAGES;
+// IRIS_DECODE_TOKEN_PAGES, a fourth bit: the head-dim kernel's token-page
+// mode (decode_hd.hip; every page size at head_dim 64-224 where
+// head_dim / 32 x num_kv_heads is even; the any-shape kernel's plan
+// elsewhere).  The caller of a page size that is not 16 m asks for it.
 // The selection bits of waves_per_block, or -1 if it is not a valid request
 // (at most one bit).
 static int32_t selection_of(int32_t waves_per_block) {
     if (waves_per_block < 0) return 0;  // (as 0: let the plan choose)
     const int32_t sel = waves_per_block & ~kWaveMask;
-    if (sel != 0 && sel != kPageKernel && sel != kValuTile && sel != kAnyKernel) return -1;
+    if (sel != 0 && sel != kPageKernel && sel != kValuTile && sel != kAnyKernel && sel != kTokenPages) return -1;
     return sel;
 }
 static bool fast_head_dim(int64_t head_dim) { return head_dim == 64 || head_dim == 128 || head_dim == 256; }
@@ -1453,9 +1458,15 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
     // head_dim 96, 160, 192 and 224: the MFMA kernel of decode_hd.hip
     // (page sizes of 16 m tokens; the others ask for the any-shape kernel).
     if (sel == 0 && hd_supported(head_dim))
-        return hd_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, max_tokens, tokens_per_split,
+        return hd_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, max_tokens, tokens_per_split, false,
                        out_chunk_tiles, out_max_chunks, out_waves, out_workspace_bytes);
-    if (sel == kAnyKernel || !fast_head_dim(head_dim)) {
+    if (sel == kTokenPages && hd_tok_supported(head_dim, num_kv_heads)) {
+        const int st = hd_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, max_tokens, tokens_per_split,
+                               true, out_chunk_tiles, out_max_chunks, out_waves, out_workspace_bytes);
+        if (st == kOk) *out_waves |= kTokenPages;
+        return st;
+    }
+    if (sel == kAnyKernel || sel == kTokenPages || !fast_head_dim(head_dim)) {
         const int st = any_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages * kPageSize, total_tokens,
                                 max_tokens, tokens_per_split, out_chunk_tiles, out_max_chunks, out_workspace_bytes);
         if (st == kOk) *out_waves = any_waves() | kAnyKernel;
@@ -1549,6 +1560,15 @@ extern "C" int iris_int4_paged_decode_attention(
         return any_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
                           workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, page_size,
                           max_pages, softmax_scale, chunk_tiles, max_chunks, stream);
+    if (sel == kTokenPages) {
+        if (page_size < 1 || max_pages <= 0 || page_size > 0x3FFFFFFF || max_pages > 0x3FFFFFFF)
+            return kInvalidArgument;
+        const int64_t pages16 = (max_pages * page_size + kPageSize - 1) / kPageSize;
+        return hd_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
+                         workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, pages16,
+                         max_pages, 0, page_size, true, softmax_scale, chunk_tiles, max_chunks,
+                         waves_of(waves_per_block), stream);
+    }
     // page_size = 16 m (m at most 16): each table entry stands for m
     // consecutive 16-token pages, so the kernels see max_pages * m of them
     // per row (the count the plan was made with); they take the page code
@@ -1567,7 +1587,8 @@ extern "C" int iris_int4_paged_decode_attention(
         if (sel != 0) return kInvalidArgument;
         return hd_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
                          workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, max_pages,
-                         bt_cols, shift, softmax_scale, chunk_tiles, max_chunks, waves, stream);
+                         bt_cols, shift, kPageSize * page_mul, false, softmax_scale, chunk_tiles, max_chunks, waves,
+                         stream);
     }
     if (waves == mqa_waves() && mqa_allowed(waves_per_block) &&
         mqa_supported(num_q_heads, num_kv_heads, head_dim) && chunk_tiles > 0)

@@ -65,8 +65,8 @@ template <int G_>
 struct Geo {
     static constexpr int G = G_, D = 32 * G_, HB = 16 * G_;  // groups, head_dim, code bytes of a head row
     // waves a workgroup and LDS slots a wave (R - 1 tiles in flight while one is computed)
-    static constexpr int W = G_ <= 3 ? 12 : 8;
-    static constexpr int R = G_ <= 5 ? 3 : 2;
+    static constexpr int W = G_ <= 2 ? 16 : G_ <= 3 ? 12 : 8;
+    static constexpr int R = G_ <= 2 ? 2 : G_ <= 5 ? 3 : 2;
     static constexpr int NK = (32 * G_ + 63) / 64;  // 16-byte loads a tensor a tile
     static constexpr int KA = 512 * G_;             // code area of a slot, per tensor (32 G pieces)
     static constexpr int SD = G_ / 2 + 1;                    // scale dwords a token needs (at most)
@@ -80,10 +80,15 @@ struct Geo {
     // Epilogue over the ring: per wave [m 16][l 16][o 16 heads x (D + 1)] fp32.
     static constexpr int EPI_ROW = D + 1, EPI_FLOATS = 32 + kHeads * EPI_ROW;
     static constexpr int CTL_OFF = W * EPI_FLOATS * 4;
-    static constexpr int LDS_BYTES = RING_BYTES > CTL_OFF + 16 ? RING_BYTES : CTL_OFF + 16;
-    static_assert(R >= 2 && R <= 4, "ring depth");
+    static constexpr int MAIN_BYTES = RING_BYTES > CTL_OFF + 16 ? RING_BYTES : CTL_OFF + 16;
+    // Token-page mode: a wave's block-table entries of two tiles (32 a tile)
+    // past the ring and the epilogue.
+    static constexpr int ID_OFF = (MAIN_BYTES + 15) / 16 * 16, ID_BYTES = 2 * 32 * 4;
+    static constexpr int LDS_BYTES = MAIN_BYTES;
+    static constexpr int LDS_BYTES_TOK = ID_OFF + W * ID_BYTES;
+    static_assert(R >= 2 && R <= 3, "ring depth");
     static_assert(NA <= SP && SD <= SP, "scale dwords of a token");
-    static_assert(LDS_BYTES <= 160 * 1024, "LDS of a CU");
+    static_assert(LDS_BYTES_TOK <= 160 * 1024, "LDS of a CU");
 };
 
 struct Args {
@@ -104,6 +109,7 @@ struct Args {
     int max_chunks, chunk_tiles;
     int max_pages;            // 16-token pages a block-table row addresses
     int bt_cols, page_code;   // block-table columns; the page code of virtual_page (page_size = 16 m)
+    int page_size;            // tokens a page (token-page mode)
     float log2_scale;
 };
 
@@ -167,6 +173,13 @@ __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
+// One dword of LDS that a direct-to-LDS load wrote, read as inline assembly
+// that waits for its own result (see Reads below).
+__device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+    return v;
+}
 __device__ __forceinline__ void store_sc1(float v, float* p) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -198,6 +211,43 @@ __device__ __forceinline__ float load_sc1(const float* p) {
 
 template <int G>
 struct Reads;
+template <>
+struct Reads<2> {
+    static __device__ __forceinline__ void k(uint32_t kb0, uint32_t kb1, uint32_t sb, uint32_t (&k)[2][2],
+                                             u32x4_t (&s)[2][2]) {
+        asm volatile(IRIS_R32(0, kb0, 0) IRIS_R32(1, kb0, 16) IRIS_R32(2, kb1, 0) IRIS_R32(3, kb1, 16)
+                         IRIS_S2(4, 5, 6, 7) IRIS_WAIT
+                     : "=&v"(k[0][0]), "=&v"(k[0][1]), "=&v"(k[1][0]), "=&v"(k[1][1]), IRIS_S2_OUT(s)
+                     : [kb0] "v"(kb0), [kb1] "v"(kb1), [sb] "v"(sb)
+                     : "memory");
+    }
+    static __device__ __forceinline__ void v(uint32_t tb, uint32_t sb, int2v_t (&v)[2], u32x4_t (&s)[2][2]) {
+        asm volatile(IRIS_TR(0, 0) IRIS_TR(1, 16) IRIS_S2(2, 3, 4, 5) IRIS_WAIT
+                     : "=&v"(v[0]), "=&v"(v[1]), IRIS_S2_OUT(s)
+                     : [tb] "v"(tb), [sb] "v"(sb)
+                     : "memory");
+    }
+};
+template <>
+struct Reads<4> {
+    static __device__ __forceinline__ void k(uint32_t kb0, uint32_t kb1, uint32_t sb, uint32_t (&k)[2][4],
+                                             u32x4_t (&s)[2][4]) {
+        asm volatile(IRIS_R32(0, kb0, 0) IRIS_R32(1, kb0, 16) IRIS_R32(2, kb0, 32) IRIS_R32(3, kb0, 48)
+                         IRIS_R32(4, kb1, 0) IRIS_R32(5, kb1, 16) IRIS_R32(6, kb1, 32) IRIS_R32(7, kb1, 48)
+                             IRIS_S4(8, 9, 10, 11, 12, 13, 14, 15) IRIS_WAIT
+                     : "=&v"(k[0][0]), "=&v"(k[0][1]), "=&v"(k[0][2]), "=&v"(k[0][3]), "=&v"(k[1][0]),
+                       "=&v"(k[1][1]), "=&v"(k[1][2]), "=&v"(k[1][3]), IRIS_S4_OUT(s)
+                     : [kb0] "v"(kb0), [kb1] "v"(kb1), [sb] "v"(sb)
+                     : "memory");
+    }
+    static __device__ __forceinline__ void v(uint32_t tb, uint32_t sb, int2v_t (&v)[4], u32x4_t (&s)[2][4]) {
+        asm volatile(IRIS_TR(0, 0) IRIS_TR(1, 16) IRIS_TR(2, 32) IRIS_TR(3, 48) IRIS_S4(4, 5, 6, 7, 8, 9, 10, 11)
+                         IRIS_WAIT
+                     : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), IRIS_S4_OUT(s)
+                     : [tb] "v"(tb), [sb] "v"(sb)
+                     : "memory");
+    }
+};
 template <>
 struct Reads<3> {
     static __device__ __forceinline__ void k(uint32_t kb0, uint32_t kb1, uint32_t sb, uint32_t (&k)[2][3],
@@ -309,7 +359,9 @@ __device__ __forceinline__ void aligned_scales(const u32x4_t (&raw)[2][Geo<G>::S
     for (int c = 0; c < Geo<G>::NA; ++c) out[c] = __builtin_amdgcn_alignbit(c + 1 < SP ? w[c + 1] : 0u, w[c], shift);
 }
 
-template <int G>
+// TOK: token-page mode (any page size; a tile's tokens looked up one by one
+// through the block table); otherwise pages of 16 m tokens.
+template <int G, bool TOK>
 __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) {
     using L = Geo<G>;
     constexpr int D = L::D, HB = L::HB, W = L::W, NK = L::NK, NS = L::NS, SP = L::SP, SLOT = L::SLOT;
@@ -346,8 +398,9 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     // ---- this wave's page ids (lane l: chunk page 2 (W (l >> 1) + wave) +
     // (l & 1), i.e. page l & 1 of its tile l >> 1, up to 32 tiles, clamped
     // into the table row), q and the length, in flight together
-    const int my_pid =
-        virtual_page(bt, min(p0 + 2 * (W * (lane >> 1) + wave) + (lane & 1), a.max_pages - 1), a.page_code);
+    int my_pid = 0;
+    if constexpr (!TOK)
+        my_pid = virtual_page(bt, min(p0 + 2 * (W * (lane >> 1) + wave) + (lane & 1), a.max_pages - 1), a.page_code);
     // q as the QK B operand: lane (head n, k-chunk jq) holds dims 32 g + 8 jq
     // .. + 7 of head n (zero for columns past the block's heads)
     const bool col_valid = n < nh;
@@ -438,9 +491,65 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
             }
         }
     };
+    if constexpr (!TOK) {
 #pragma unroll
-    for (int s = 0; s < L::R - 1; ++s)
-        if (s < n_my) issue(s, s);
+        for (int s = 0; s < L::R - 1; ++s)
+            if (s < n_my) issue(s, s);
+    }
+
+    // ---- token-page mode: a tile's 32 tokens (the last valid one for those
+    // past the sequence) are looked up one by one.  Lane l < 32 loads the
+    // block-table entry of token l into the wave's entry slot (tile & 1),
+    // one tile before the tile's data loads; then each lane turns its entry
+    // into the token's slot in the pool (entry * page_size + token %
+    // page_size) and every load lane takes its token's slot with
+    // ds_bpermute.  The scale shift of a token is uniform because the mode
+    // is taken only where Hkv * G is even.
+    uint8_t* const ent_base = smem + L::ID_OFF + wave * L::ID_BYTES;
+    const int psz = a.page_size;
+    auto issue_entries = [&](int s) __attribute__((always_inline)) {
+        const int tg = min((t_begin + W * s + wave) * kTile + lane, seq_len - 1);
+        if (lane < 32)
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(bt + min(tg / psz, a.bt_cols - 1)),
+                                             (IRIS_LDS void*)(ent_base + (s & 1) * 128), 4, 0, 0);
+    };
+    auto slots_of = [&](int s) __attribute__((always_inline)) -> uint32_t {
+        const uint32_t e = lds_read_b32(lds_addr(ent_base + (s & 1) * 128) + 4 * (lane & 31));
+        const int tg = min((t_begin + W * s + wave) * kTile + (lane & 31), seq_len - 1);
+        return e * (uint32_t)psz + (uint32_t)(tg % psz);  // a pool of at most 2^32 token slots
+    };
+    const int64_t row_bytes = (int64_t)a.n_kv_heads * HB;       // a token row of a code tensor
+    const int64_t srow_halves = (int64_t)a.n_kv_heads * G;      // a token row of a scale tensor
+    const int tok_sh = (kvh * G) & 1;                           // (Hkv * G even)
+    auto issue_tok = [&](int slot, uint32_t slots) __attribute__((always_inline)) {
+        uint8_t* const dst = ring + slot * SLOT;
+#pragma unroll
+        for (int i = 0; i < NK; ++i) {
+            const int p = 64 * i + lane;
+            const int m = (p < 32 * G ? p : 0) / G, c = p - (p / G) * G;
+            const uint32_t sm = __builtin_amdgcn_ds_bpermute(4 * m, (int)slots);  // every lane, outside the branch
+            if (NK * 64 == 32 * G || p < 32 * G) {
+                const int64_t off = (int64_t)sm * row_bytes + kvh * HB + 16 * c;
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.k_data + off),
+                                                 (IRIS_LDS void*)(dst + L::K_OFF + 1024 * i), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.v_data + off),
+                                                 (IRIS_LDS void*)(dst + L::V_OFF + 1024 * i), 16, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NS; ++i) {
+            const int p = 64 * i + lane;
+            const int t = p / SP, j = p % SP;
+            const uint32_t st = __builtin_amdgcn_ds_bpermute(4 * t, (int)slots);
+            if (sc_ok[i]) {
+                const int64_t off = (((int64_t)st * srow_halves + kvh * G) - tok_sh) * 2 + 4 * j;
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.k_scale + off),
+                                                 (IRIS_LDS void*)(dst + L::KS_OFF + 256 * i), 4, 0, 0);
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.v_scale + off),
+                                                 (IRIS_LDS void*)(dst + L::VS_OFF + 256 * i), 4, 0, 0);
+            }
+        }
+    };
 
     // ---- q operands (in the order of k_operand; high-nibble dims / 16) and
     // the accumulator start that removes the +8 of the K codes: C row (token)
@@ -608,23 +717,65 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     // always JOBS of them), with tiles s + 1 .. s + R - 1 in flight; slot
     // (s - 1) % R, whose reads by tile s - 1 have returned, receives tile
     // s + R - 1 first.
+    //
+    // Token-page mode: per tile one more load (its block-table entries), the
+    // entries one tile ahead of the data: iteration s reads the entries of
+    // tile s + R - 1 (loaded at s - 1, before the data of tile s + R - 2),
+    // issues the entries of tile s + R, then the data of tile s + R - 1.
     constexpr int R = L::R;
     constexpr int JOBS = 2 * NK + 2 * NS;
-    static_assert((R - 1) * JOBS < 64, "vmcnt range");
+    static_assert((R - 1) * JOBS + 2 < 64, "vmcnt range");
     const uint32_t ring_addr = lds_addr(ring);
     int slot_c = 0;          // slot of tile s
     int slot_i = R - 1;      // slot of tile s + R - 1
+    if constexpr (TOK) {
+        // entries of tiles 0 and 1, then data 0, (R = 3: entries 2,) data 1
+        if (n_my > 0) issue_entries(0);
+        if (n_my > 1) issue_entries(1);
+        wait_vmcnt<0>();
+        if (n_my > 0) issue_tok(0, slots_of(0));
+        if constexpr (R == 3) {
+            if (n_my > 2) issue_entries(2);
+            if (n_my > 1) issue_tok(1, slots_of(1));
+        }
+    }
     for (int s = 0; s < n_my; ++s) {
         const int ahead = min(n_my - 1 - s, R - 1);  // tiles in flight behind tile s
-        if (ahead == R - 1) {
-            issue(s + R - 1, slot_i);
-            wait_vmcnt<(R - 1) * JOBS>();
-        } else if (R > 3 && ahead == 2) {
-            wait_vmcnt<2 * JOBS>();
-        } else if (R > 2 && ahead == 1) {
-            wait_vmcnt<JOBS>();
+        if constexpr (!TOK) {
+            if (ahead == R - 1) {
+                issue(s + R - 1, slot_i);
+                wait_vmcnt<(R - 1) * JOBS>();
+            } else if (R > 2 && ahead == 1) {
+                wait_vmcnt<JOBS>();
+            } else {
+                wait_vmcnt<0>();
+            }
+        } else if constexpr (R == 2) {
+            if (ahead == 1) {
+                wait_vmcnt<JOBS>();  // the entries of tile s + 1 (tile s's data may fly)
+                const int sl = slots_of(s + 1);
+                if (s + 2 < n_my) {
+                    issue_entries(s + 2);
+                    issue_tok(slot_i, sl);
+                    wait_vmcnt<JOBS + 1>();  // tile s
+                } else {
+                    issue_tok(slot_i, sl);
+                    wait_vmcnt<JOBS>();
+                }
+            } else {
+                wait_vmcnt<0>();
+            }
         } else {
-            wait_vmcnt<0>();
+            if (ahead == 2) {
+                wait_vmcnt<JOBS>();  // tile s and the entries of tile s + 2 (tile s + 1 flies)
+                const int sl = slots_of(s + 2);
+                if (s + 3 < n_my) issue_entries(s + 3);
+                issue_tok(slot_i, sl);
+            } else if (ahead == 1) {
+                wait_vmcnt<JOBS>();  // tile s
+            } else {
+                wait_vmcnt<0>();
+            }
         }
         compute(t_begin + W * s + wave, ring_addr + (uint32_t)(slot_c * SLOT));
         slot_c = slot_c == R - 1 ? 0 : slot_c + 1;
@@ -760,9 +911,18 @@ bool hd_supported(int64_t head_dim) {
     return head_dim == 96 || head_dim == 160 || head_dim == 192 || head_dim == 224;
 }
 
+bool hd_tok_supported(int64_t head_dim, int64_t num_kv_heads) {
+    // A token's scale row (Hkv G halves) is a whole number of dwords, so
+    // every token's kv head starts on the same half.
+    return head_dim % 32 == 0 && head_dim >= 64 && head_dim <= 224 && num_kv_heads > 0 &&
+           (head_dim / 32 * num_kv_heads) % 2 == 0;
+}
+
 int hd_waves(int64_t head_dim) {
     switch (head_dim) {
+        case 64: return hd::Geo<2>::W;
         case 96: return hd::Geo<3>::W;
+        case 128: return hd::Geo<4>::W;
         case 160: return hd::Geo<5>::W;
         case 192: return hd::Geo<6>::W;
         default: return hd::Geo<7>::W;
@@ -779,10 +939,10 @@ static int64_t hd_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t he
 }
 
 int hd_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t max_pages,
-            int64_t max_tokens, int32_t tokens_per_split, int32_t* out_chunk_tiles, int32_t* out_max_chunks,
-            int32_t* out_waves, int64_t* out_workspace_bytes) {
-    if (!hd_supported(head_dim) || batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
-        max_pages <= 0)
+            int64_t max_tokens, int32_t tokens_per_split, bool token_pages, int32_t* out_chunk_tiles,
+            int32_t* out_max_chunks, int32_t* out_waves, int64_t* out_workspace_bytes) {
+    const bool ok = token_pages ? hd_tok_supported(head_dim, num_kv_heads) : hd_supported(head_dim);
+    if (!ok || batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || max_pages <= 0)
         return kInvalidArgument;
     const int64_t q_blocks = (num_q_heads / num_kv_heads + hd::kHeads - 1) / hd::kHeads;
     const int W = hd_waves(head_dim);
@@ -820,13 +980,14 @@ int hd_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t he
 }
 
 namespace {
-template <int G>
+template <int G, bool TOK>
 int launch_hd(dim3 grid, hipStream_t s, const hd::Args& a) {
     using L = hd::Geo<G>;
     static std::atomic<uint64_t> lds_raised{0};
-    if (allow_full_lds(reinterpret_cast<const void*>(&hd::int4_decode_hd_kernel<G>), lds_raised) != kOk)
+    if (allow_full_lds(reinterpret_cast<const void*>(&hd::int4_decode_hd_kernel<G, TOK>), lds_raised) != kOk)
         return kLaunchError;
-    hipLaunchKernelGGL((hd::int4_decode_hd_kernel<G>), grid, dim3(64 * L::W), L::LDS_BYTES, s, a);
+    hipLaunchKernelGGL((hd::int4_decode_hd_kernel<G, TOK>), grid, dim3(64 * L::W), TOK ? L::LDS_BYTES_TOK : L::LDS_BYTES,
+                       s, a);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchError;
 }
 }  // namespace
@@ -835,15 +996,21 @@ int hd_launch(const void* query, const void* k_data, const void* v_data, const v
               const int32_t* block_table, const int32_t* seq_lens, void* output, int32_t output_is_f32,
               void* workspace, int64_t workspace_bytes_avail, int64_t batch, int64_t num_q_heads,
               int64_t num_kv_heads, int64_t head_dim, int64_t max_pages, int64_t bt_cols, int32_t page_code,
-              float softmax_scale, int32_t chunk_tiles, int32_t max_chunks, int32_t waves, void* stream) {
-    if (!hd_supported(head_dim) || batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 ||
-        max_pages <= 0)
+              int64_t page_size, bool token_pages, float softmax_scale, int32_t chunk_tiles, int32_t max_chunks,
+              int32_t waves, void* stream) {
+    const bool ok = token_pages ? hd_tok_supported(head_dim, num_kv_heads) && page_size >= 1 && bt_cols > 0 &&
+                                      bt_cols * page_size <= 0x3FFFFFFF
+                                : hd_supported(head_dim);
+    if (!ok || batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || max_pages <= 0)
         return kInvalidArgument;
     const int W = hd_waves(head_dim);
     if (waves != W || chunk_tiles <= 0 || chunk_tiles > hd_max_chunk_tiles(W) || max_chunks <= 0 ||
         max_chunks > hd::kMaxChunks)
         return kInvalidArgument;
-    if ((int64_t)chunk_tiles * max_chunks * 2 < max_pages) return kInvalidArgument;  // the grid covers every page
+    // the grid covers every token (every 16-token page) the table addresses
+    if (token_pages ? (int64_t)chunk_tiles * max_chunks * hd::kTile < bt_cols * page_size
+                    : (int64_t)chunk_tiles * max_chunks * 2 < max_pages)
+        return kInvalidArgument;
     const int64_t g = num_q_heads / num_kv_heads;
     const int64_t q_blocks = (g + hd::kHeads - 1) / hd::kHeads;
     if (max_chunks > 1 && num_kv_heads * q_blocks > kCountersPerSeq) return kInvalidArgument;
@@ -870,6 +1037,7 @@ int hd_launch(const void* query, const void* k_data, const void* v_data, const v
     a.max_pages = (int)max_pages;
     a.bt_cols = (int)bt_cols;
     a.page_code = page_code;
+    a.page_size = (int)page_size;
     a.log2_scale = softmax_scale * 1.4426950408889634f;
     a.counters = nullptr;
     a.part_o = a.part_ml = nullptr;
@@ -884,11 +1052,21 @@ int hd_launch(const void* query, const void* k_data, const void* v_data, const v
     }
     const dim3 grid((unsigned)nblocks);
     hipStream_t s = (hipStream_t)stream;
+    if (token_pages) {
+        switch (head_dim) {
+            case 64: return launch_hd<2, true>(grid, s, a);
+            case 96: return launch_hd<3, true>(grid, s, a);
+            case 128: return launch_hd<4, true>(grid, s, a);
+            case 160: return launch_hd<5, true>(grid, s, a);
+            case 192: return launch_hd<6, true>(grid, s, a);
+            default: return launch_hd<7, true>(grid, s, a);
+        }
+    }
     switch (head_dim) {
-        case 96: return launch_hd<3>(grid, s, a);
-        case 160: return launch_hd<5>(grid, s, a);
-        case 192: return launch_hd<6>(grid, s, a);
-        default: return launch_hd<7>(grid, s, a);
+        case 96: return launch_hd<3, false>(grid, s, a);
+        case 160: return launch_hd<5, false>(grid, s, a);
+        case 192: return launch_hd<6, false>(grid, s, a);
+        default: return launch_hd<7, false>(grid, s, a);
     }
 }
 

@@ -35,7 +35,8 @@ from . import _lib
 
 __all__ = ["fused_int4_paged_decode_attention", "_int4_paged_decode_attention", "decode_plan",
            "fused_fp16_paged_decode_attention", "_fp16_paged_decode_attention", "fp16_decode_plan",
-           "DECODE_PAGE_KERNEL", "DECODE_VALU_TILE", "DECODE_ANY_KERNEL", "int4_decode_plan"]
+           "DECODE_PAGE_KERNEL", "DECODE_VALU_TILE", "DECODE_ANY_KERNEL", "DECODE_TOKEN_PAGES",
+           "int4_decode_plan"]
 
 # Kernel selection bits or-ed into ``waves_per_block`` (IRIS_DECODE_PAGE_KERNEL
 # and IRIS_DECODE_VALU_TILE of include/iris_hip.h), for A/B measurements and
@@ -48,8 +49,13 @@ DECODE_VALU_TILE = 0x200
 # multiple of 32 up to 512, every page size.  The plan picks it by itself for
 # head dims other than 64, 96, 128, 160, 192, 224 and 256 (96-224 have an
 # MFMA kernel of their own); page sizes that are not a multiple of 16 up to
-# 256 must ask for it.
+# 256 ask for it or for DECODE_TOKEN_PAGES.
 DECODE_ANY_KERNEL = 0x400
+# The token-page mode of the head-dim MFMA kernel (IRIS_DECODE_TOKEN_PAGES):
+# every page size, each token's page looked up through the block table, at
+# head_dim 64 to 224 (steps of 32) where head_dim / 32 * num_kv_heads is
+# even; asked for at other shapes, the plan returns the any-shape kernel's.
+DECODE_TOKEN_PAGES = 0x800
 
 
 def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, max_pages: int,
@@ -59,7 +65,7 @@ def decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int, 
 
     ``max_pages`` counts 16-token pages: ceil(block_table columns * page_size / 16).
     For page sizes that are not a multiple of 16 up to 256 use
-    ``int4_decode_plan``, which asks for the any-shape kernel."""
+    ``int4_decode_plan``, which asks for the token-page mode."""
     ct, mc, nw = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
     ws = ctypes.c_int64()
     status = _lib.lib().iris_decode_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages,
@@ -81,10 +87,13 @@ def int4_decode_plan(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: 
                      waves_per_block: int = 0) -> tuple[int, int, int, int]:
     """The decode plan for a cache of ``page_size``-token pages and a block
     table ``bt_cols`` columns wide: ``decode_plan`` over the tokens a row
-    addresses, with the any-shape kernel asked for when the page size is not
-    a multiple of 16 up to 256."""
+    addresses.  A page size that is not a multiple of 16 up to 256 asks for
+    the token-page mode (which falls back to the any-shape kernel at shapes
+    it does not take), or keeps DECODE_ANY_KERNEL if the caller asked for
+    that."""
     if not _fast_page_size(page_size):
-        waves_per_block = (max(waves_per_block, 0) & 0xFF) | DECODE_ANY_KERNEL
+        sel = DECODE_ANY_KERNEL if waves_per_block > 0 and waves_per_block & DECODE_ANY_KERNEL else DECODE_TOKEN_PAGES
+        waves_per_block = (max(waves_per_block, 0) & 0xFF) | sel
     return decode_plan(batch, num_q_heads, num_kv_heads, head_dim, -(-bt_cols * page_size // 16), total_tokens,
                        max_tokens, tokens_per_split, waves_per_block)
 

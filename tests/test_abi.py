@@ -91,6 +91,19 @@ def test_decode_rejects_unsupported_shapes_before_launch():
     assert call(P=48, nw=any_, ct=3, mc=4) == 1             # chunks of whole 64-token tiles
     assert call(P=48, nw=any_, ct=2, mc=3) == 3             # three chunks need a workspace
     assert call(nw=0x400 | 0x100) == 1                      # one selection bit at most
+    assert call(nw=0x800 | 0x400) == 1
+    # the token-page mode: any page size, head_dim 64-224 with D / 32 x Hkv even
+    tok = 0x800
+    assert call(D=96, P=24, nw=12 | tok, ct=12, mc=1) == 2   # valid: it gets as far as the launch
+    assert call(D=64, P=1, nw=16 | tok, ct=16, mc=1) == 2
+    assert call(D=128, P=8, nw=8 | tok, ct=8, mc=1) == 2
+    assert call(D=224, P=16, nw=8 | tok, ct=8, mc=1) == 2   # 16-token pages too
+    assert call(D=96, P=24, Hkv=1, nw=12 | tok, ct=12, mc=1) == 1  # 3 x 1 scale halves a row: odd
+    assert call(D=256, P=8, nw=8 | tok, ct=8, mc=1) == 1    # head_dim 64 to 224
+    assert call(D=96, P=24, nw=8 | tok, ct=12, mc=1) == 1   # its wave count only
+    assert call(D=96, P=0, nw=12 | tok, ct=12, mc=1) == 1   # page_size >= 1
+    assert call(D=96, P=200, nw=12 | tok, ct=12, mc=2) == 1  # chunks do not cover 4 x 200 tokens
+    assert call(D=96, P=200, nw=12 | tok, ct=24, mc=2) == 3  # two chunks need a workspace
     assert call(Hq=9) == 1          # Hq not divisible by Hkv
     assert call(ct=1, mc=1) == 1    # chunks do not cover max_pages
     assert call(nw=5) == 1
@@ -296,17 +309,36 @@ def test_decode_plan_overrides_and_errors():
     for bad in (80, 544, 0):
         with pytest.raises(RuntimeError):
             decode_plan(2, 8, 2, bad, 64)
+    # the token-page mode when asked: the head-dim kernel's waves (16 at 64,
+    # 12 at 96, 8 above) and its workspace layout; the any-shape kernel's
+    # plan where it does not take the shape
+    assert decode_plan(2, 8, 2, 128, 64, waves_per_block=0x800)[2] == 8 | 0x800
+    assert decode_plan(2, 8, 2, 64, 64, waves_per_block=0x800)[2] == 16 | 0x800
+    assert decode_plan(2, 8, 1, 64, 64, waves_per_block=0x800)[2] == 16 | 0x800
+    assert decode_plan(2, 8, 2, 96, 64, waves_per_block=0x800)[2] == 12 | 0x800
+    assert decode_plan(2, 8, 1, 96, 64, waves_per_block=0x800)[2] == 4 | 0x400   # 3 halves a row
+    assert decode_plan(2, 8, 2, 256, 64, waves_per_block=0x800)[2] == 4 | 0x400
+    assert decode_plan(2, 8, 2, 288, 64, waves_per_block=0x800)[2] == 4 | 0x400
+    ct, mc, nw, ws = decode_plan(2, 8, 2, 160, 64, tokens_per_split=256, waves_per_block=0x800)
+    assert (ct, mc, nw) == (8, 4, 8 | 0x800), (ct, mc, nw)
+    assert ws == any_workspace(2, 8, 160, 4)
     # page sizes that are not a multiple of 16 up to 256: int4_decode_plan
-    # asks for the any-shape kernel; multiples of 16 (48, 80, ...) plan the
-    # fast kernels over 16-token pages
+    # asks for the token-page mode (the any-shape kernel where that does
+    # not take the shape, or when the caller asks for it); multiples of 16
+    # (48, 80, ...) plan the fast kernels over 16-token pages
     from iris_kernel.fused_attention import int4_decode_plan
 
-    assert int4_decode_plan(2, 8, 2, 128, 24, 10)[2] == 4 | 0x400
-    assert int4_decode_plan(2, 8, 2, 128, 1, 1000)[2] == 4 | 0x400
-    assert int4_decode_plan(2, 8, 2, 128, 272, 10)[2] == 4 | 0x400
+    assert int4_decode_plan(2, 8, 2, 128, 24, 10)[2] == 8 | 0x800
+    assert int4_decode_plan(2, 8, 2, 128, 1, 1000)[2] == 8 | 0x800
+    assert int4_decode_plan(2, 8, 2, 128, 272, 10)[2] == 8 | 0x800
+    assert int4_decode_plan(2, 8, 1, 96, 24, 10)[2] == 4 | 0x400
+    assert int4_decode_plan(2, 8, 2, 256, 24, 10)[2] == 4 | 0x400
+    assert int4_decode_plan(2, 8, 2, 128, 24, 10, waves_per_block=0x400)[2] == 4 | 0x400
     assert int4_decode_plan(2, 8, 2, 128, 32, 10)[2] in (4, 16)
     assert int4_decode_plan(2, 8, 2, 128, 48, 10)[2] in (1, 2, 3, 4, 16)
     ct, mc, nw, ws = int4_decode_plan(3, 8, 2, 128, 8, 60, tokens_per_split=64)
+    assert ct * 32 * mc >= 60 * 8 and ct % 8 == 0 and nw == 8 | 0x800
+    ct, mc, nw, ws = int4_decode_plan(3, 8, 2, 128, 8, 60, tokens_per_split=64, waves_per_block=0x400)
     assert ct * 32 * mc >= 60 * 8 and ct % 2 == 0 and nw & 0x400
 
 
@@ -358,7 +390,9 @@ def test_decode_kernel_selection_bits(monkeypatch):
     with pytest.raises(RuntimeError):
         decode_plan(*shape, waves_per_block=DECODE_PAGE_KERNEL | DECODE_VALU_TILE)
     with pytest.raises(RuntimeError):
-        decode_plan(*shape, waves_per_block=0x800)
+        decode_plan(*shape, waves_per_block=0x1000)
+    with pytest.raises(RuntimeError):
+        decode_plan(*shape, waves_per_block=0x800 | 0x400)
 
 
 def test_valu_tile_selection_covers_two_layouts():

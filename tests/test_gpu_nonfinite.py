@@ -15,8 +15,8 @@ the codes' +8 offset by a second sum, give NaN: both are non-finite.)
 Each case is run on the plan's own choice, on each INT4 kernel forced (the
 streaming kernel at its shapes (4 and 8 query heads per kv head), the MQA
 kernel at its shape, the page kernel,
-the general kernel and its VALU tile, the kernel of head_dim 96 to 224, the
-any-shape kernel), with one chunk a sequence and with
+the general kernel and its VALU tile, the kernel of head_dim 96 to 224 and
+its token-page mode, the any-shape kernel), with one chunk a sequence and with
 split-KV, and on a cache the package's own append wrote from an infinite key
 and value.  The FP16-cache decode gets the same check with NaN / Inf cache
 values."""
@@ -25,7 +25,7 @@ import torch
 
 from helpers import ATOL, log, to
 from iris_kernel import workloads
-from iris_kernel.fused_attention import (DECODE_ANY_KERNEL, DECODE_PAGE_KERNEL, DECODE_VALU_TILE,
+from iris_kernel.fused_attention import (DECODE_ANY_KERNEL, DECODE_PAGE_KERNEL, DECODE_TOKEN_PAGES, DECODE_VALU_TILE,
                                          fused_fp16_paged_decode_attention, fused_int4_paged_decode_attention)
 from iris_kernel.fused_kv import fused_rope_int4_paged_append
 from oracle.torch_eager_attention import (torch_eager_fp16_paged_decode_attention,
@@ -57,6 +57,8 @@ KERNELS = [
     ("d96-hd", 8, 2, 96, 0),
     ("d224-hd", 12, 3, 224, 0),
     ("d96-any", 8, 2, 96, DECODE_ANY_KERNEL),
+    ("gqa-tok", 32, 8, 128, DECODE_TOKEN_PAGES),
+    ("d96-tok", 8, 2, 96, DECODE_TOKEN_PAGES),
 ]
 
 # (name, what is poisoned): sequence b, token t < L_b, kv head, scale group.

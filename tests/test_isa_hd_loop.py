@@ -1,10 +1,12 @@
 """The head_dim 96-224 decode kernel's tile loop, checked in its compiled
-gfx950 code (csrc/decode_hd.hip, every G instance).
+gfx950 code (csrc/decode_hd.hip, every G instance of both modes: pages of
+16 m tokens, and token pages at head_dim 64-224).
 
 A wave keeps R - 1 tiles' direct-to-LDS loads in flight while it computes
 one, which holds only if every vmcnt wait in the loop is one of the kernel's
-own (a multiple of one tile's load instructions: the compiler would
-otherwise wait for the loads streaming into the other slots).  Two
+own (a multiple of one tile's load instructions, plus, in token-page mode,
+the one load of a tile's block-table entries: the compiler would otherwise
+wait for the loads streaming into the other slots).  Two
 regressions this guards against, both seen while the kernel was written: the
 loop compiled as a divergent loop (its bounds in VGPRs, an exec-mask exit
 around every tile), and spilled registers.  Compiles decode_hd.hip once
@@ -20,6 +22,14 @@ from iris_kernel import _build
 
 SRC = _build.CSRC / "decode_hd.hip"
 GROUPS = [3, 5, 6, 7]  # head_dim / 32
+INSTANCES = [(g, False) for g in GROUPS] + [(g, True) for g in (2, 3, 4, 5, 6, 7)]
+
+
+def jobs_of(g: int) -> int:
+    """Load instructions of one tile: 16-byte code loads (32 g pieces of 64
+    lanes) and 4-byte scale loads (2 or 4 dwords a token), for K and V."""
+    sp = 2 if g // 2 + 1 <= 2 else 4
+    return 2 * ((32 * g + 63) // 64) + 2 * (32 * sp // 64)
 
 
 @pytest.fixture(scope="module")
@@ -38,8 +48,8 @@ def asm(tmp_path_factory):
     return out.read_text()
 
 
-def kernel(asm: str, g: int) -> list[str]:
-    sym = f"_ZN4iris2hd21int4_decode_hd_kernelILi{g}EEEvNS0_4ArgsE"
+def kernel(asm: str, g: int, tok: bool) -> list[str]:
+    sym = f"_ZN4iris2hd21int4_decode_hd_kernelILi{g}ELb{int(tok)}EEEvNS0_4ArgsE"
     body = asm[asm.index(sym + ":"):]
     body = body[:body.index(".Lfunc_end")]
     return [l.strip() for l in body.split("\n")]
@@ -59,27 +69,34 @@ def tile_loop(lines: list[str]) -> list[str]:
     return out
 
 
-@pytest.mark.parametrize("g", GROUPS)
-def test_tile_loop_is_the_tile_loop(asm, g):
-    loop = tile_loop(kernel(asm, g))
+@pytest.mark.parametrize("g,tok", INSTANCES)
+def test_tile_loop_is_the_tile_loop(asm, g, tok):
+    loop = tile_loop(kernel(asm, g, tok))
     # per tile: 2 G QK and 2 G PV products, G transposed V reads
     assert sum(1 for l in loop if l.startswith("v_mfma")) == 4 * g
     assert sum(1 for l in loop if l.startswith("ds_read_b64_tr_b8")) == g
 
 
-@pytest.mark.parametrize("g", GROUPS)
-def test_tile_loop_waits_only_for_its_own_tiles(asm, g):
-    loop = tile_loop(kernel(asm, g))
-    jobs = sum(1 for l in loop if l.startswith("global_load_lds"))  # one tile's loads (issued once a step)
-    assert jobs >= 2 * ((32 * g + 63) // 64) + 2, jobs
+@pytest.mark.parametrize("g,tok", INSTANCES)
+def test_tile_loop_waits_only_for_its_own_tiles(asm, g, tok):
+    loop = tile_loop(kernel(asm, g, tok))
+    jobs = jobs_of(g)
+    loads = sum(1 for l in loop if l.startswith("global_load_lds"))
     waits = {int(m) for l in loop if l.startswith("s_waitcnt") for m in re.findall(r"vmcnt\((\d+)\)", l)}
     assert 0 in waits and len(waits) >= 2, waits
-    assert all(w % jobs == 0 and w < 64 for w in waits), (jobs, sorted(waits))
+    if not tok:
+        assert loads == jobs, (loads, jobs)  # one tile's loads, issued once a step
+        assert all(w % jobs == 0 and w < 64 for w in waits), (jobs, sorted(waits))
+    else:
+        # a tile's data loads (in one or two copies of the issue) and the
+        # next entries' one load; waits for a tile or a tile and the entries
+        assert loads in (jobs + 1, 2 * jobs + 1), (loads, jobs)
+        assert waits <= {0, jobs, jobs + 1}, (jobs, sorted(waits))
 
 
-@pytest.mark.parametrize("g", GROUPS)
-def test_tile_loop_is_uniform_and_nothing_spills(asm, g):
-    lines = kernel(asm, g)
+@pytest.mark.parametrize("g,tok", INSTANCES)
+def test_tile_loop_is_uniform_and_nothing_spills(asm, g, tok):
+    lines = kernel(asm, g, tok)
     loop = tile_loop(lines)
     assert not [l for l in loop if re.match(r"s_andn2_b64\s+exec, exec", l)]  # no divergent-loop exit
     assert not [l for l in loop if l.startswith("v_readfirstlane")]
