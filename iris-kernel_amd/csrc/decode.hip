@@ -1411,6 +1411,10 @@ static bool pages_preferred(int64_t batch, int64_t num_q_heads, int64_t num_kv_h
     // page kernel's g=8 layout is slower there than the general kernel.
     if (num_q_heads == 8 * num_kv_heads && stream_supported(num_q_heads, num_kv_heads, head_dim)) {
         if (page_kernel || max_pages * kPageSize > (int64_t)stream_max_chunks() * 64 * kTile) return false;
+        // One or two sequences give its chunk mode too few workgroups
+        // (MI355X, L=131072: B=1 100.3 us against 57.0 on the general
+        // kernel; B=2 102.1 against 79.9; B=3, L=65536: 63.2 against 64.8).
+        if (batch < 3) return false;
         if (total_tokens * num_kv_heads * (head_dim + head_dim / 8) < kPagesMinBytes) return false;
         return 4 * total_tokens >= 3 * batch * max_tokens;
     }
@@ -1440,6 +1444,28 @@ static bool mqa_allowed(int32_t waves_per_block) {
 static bool mqa_preferred(int64_t batch, int64_t total_tokens, int64_t max_tokens) {
     if (total_tokens * (64 + 8) < kMqaMinBytes) return false;
     return 4 * total_tokens >= 3 * batch * max_tokens;
+}
+
+// head_dim 64 and 128 at mid sizes: the head-dim kernel (decode_hd.hip) in
+// its token-page mode takes the shapes the plan would give the general
+// kernel when they read between kHdMinBytes and kPagesMinBytes of K/V over
+// batches of similar lengths in at most 256 (sequence, kv head, query block)
+// units -- its W-wave workgroups stream a unit's tiles with no workgroup
+// barrier and its grid follows the XCDs (MI355X, interleaved: B=4, L=8192,
+// Hkv=8: 22.6 against 25.5 us; B=32, L=2048: 29.7 against 33.1; D=64,
+// Hq=32, Hkv=8, B=32, L=2048: 20.8 against 25.8; B=1, L=32768: 26.1 against
+// 49.9).  Smaller launches are latency-bound and come out even or slower,
+// and more units (B=64, L=1024: 34.9 against 33.0) or ragged lengths (B=64,
+// lengths in [16, 4096]: 51.3 against 43.1) favour the general kernel's
+// smaller workgroups.
+constexpr int64_t kHdMinBytes = 4000000;
+static bool hd_preferred(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                         int64_t total_tokens, int64_t max_tokens) {
+    if (head_dim != 64 && head_dim != 128) return false;
+    const int64_t units = batch * num_kv_heads * query_blocks((int)(num_q_heads / num_kv_heads));
+    const int64_t bytes = total_tokens * num_kv_heads * (head_dim + head_dim / 8);
+    return units <= 256 && bytes >= kHdMinBytes && bytes < kPagesMinBytes &&
+           4 * total_tokens >= 3 * batch * max_tokens;
 }
 
 // Split plan for one decode call.  total_tokens / max_tokens may be -1 when
@@ -1489,6 +1515,13 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
                                   tokens_per_split, (sel & kPageKernel) == 0, out_chunk_tiles, out_max_chunks,
                                   out_waves, out_workspace_bytes);
         if (st == kOk) *out_waves |= sel & kPageKernel;
+        return st;
+    }
+    if (sel == 0 && waves_of(waves_per_block) == 0 &&
+        hd_preferred(batch, num_q_heads, num_kv_heads, head_dim, est_total, est_max)) {
+        const int st = hd_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, max_tokens, tokens_per_split,
+                               true, out_chunk_tiles, out_max_chunks, out_waves, out_workspace_bytes);
+        if (st == kOk) *out_waves |= kTokenPages;
         return st;
     }
     const int g = (int)(num_q_heads / num_kv_heads);

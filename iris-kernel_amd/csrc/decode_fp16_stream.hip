@@ -177,8 +177,7 @@ __device__ __forceinline__ float rows_sum(float x) {
     return __builtin_bit_cast(float, c) + __builtin_bit_cast(float, d);
 }
 
-// The scalars the prologue needs come first, as separate arguments (built
-// with -mllvm -amdgpu-kernarg-preload-count=6 they arrive in SGPRs).
+// The scalars the prologue needs come first, as separate arguments.
 template <int D>
 __global__ __launch_bounds__(1024) void fp16_decode_stream_kernel(const int32_t* p_seq_lens,
                                                                   const int32_t* p_block_table, int p_max_chunks,
@@ -198,7 +197,11 @@ __global__ __launch_bounds__(1024) void fp16_decode_stream_kernel(const int32_t*
     const int rowb = cpr * 16;          // bytes of a token row
     const int g = a.group;
 
-    const int b = blockIdx.x / p_max_chunks, chunk = blockIdx.x % p_max_chunks;
+    // chunk slowest (the grid is batch x max_chunks): each XCD (workgroup i
+    // runs on XCD i % 8) gets its share of every chunk index, so chunks past
+    // the sequences' ends, which return at once, leave no XCD idle
+    const int batch = gridDim.x / p_max_chunks;
+    const int chunk = blockIdx.x / batch, b = blockIdx.x - chunk * batch;
     const int p0 = chunk * p_chunk_pages;
     const int32_t* bt = p_block_table + (int64_t)b * p_max_pages;
     // page ids of the chunk: logical page p0 + i in lane i of pid0 / pid1

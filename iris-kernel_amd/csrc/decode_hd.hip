@@ -105,7 +105,8 @@ struct Args {
     float* part_ml;      // [B][max_chunks][Hq][2] (m, l), base-2 logits
     int out_f32;
     int n_q_heads, n_kv_heads, group, q_blocks;
-    int n_units;  // batch x q_blocks x max_chunks
+    int n_units;    // batch x q_blocks x max_chunks
+    int seq_units;  // batch x q_blocks: the units of one chunk index
     int max_chunks, chunk_tiles;
     int max_pages;            // 16-token pages a block-table row addresses
     int bt_cols, page_code;   // block-table columns; the page code of virtual_page (page_size = 16 m)
@@ -371,21 +372,24 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     const int n = lane & 15;   // MFMA row (A) or column (B, C): token or query head
     const int jq = lane >> 4;  // MFMA k-chunk (A, B) or row quad (C)
 
-    // ---- (kv head, unit = (sequence b, query block, chunk)).  Workgroups
-    // are dispatched to the 8 XCDs in turn (workgroup i to XCD i % 8), and a
-    // kv head's rows are only 16 G of each token's Hkv 16 G bytes: the kv
-    // heads of one unit run on one XCD, one after another (k = i / 8, unit
-    // (k / Hkv) 8 + i % 8, kv head k % Hkv), so the cache lines they share
-    // are fetched into one L2.  The grid is padded to whole groups of 8
-    // units; padding workgroups return at once.  The divisions run on the
-    // VALU; readfirstlane keeps the results, and all that derives from them
-    // (the loop bounds among it), scalar.
+    // ---- (kv head, unit = (chunk, sequence b, query block), chunk
+    // slowest).  Workgroups are dispatched to the 8 XCDs in turn (workgroup
+    // i to XCD i % 8), and a kv head's rows are only 16 G of each token's
+    // Hkv 16 G bytes: the kv heads of one unit run on one XCD, one after
+    // another (k = i / 8, unit (k / Hkv) 8 + i % 8, kv head k % Hkv), so the
+    // cache lines they share are fetched into one L2.  With the chunk index
+    // slowest, each XCD gets its share of every chunk index (chunks past a
+    // sequence's end, which return at once, would otherwise leave whole XCDs
+    // idle when the table is wider than the sequences).  The grid is padded
+    // to whole groups of 8 units; padding workgroups return at once.  The
+    // divisions run on the VALU; readfirstlane keeps the results, and all
+    // that derives from them (the loop bounds among it), scalar.
     const int k_x = blockIdx.x >> 3;
     const int kvh = __builtin_amdgcn_readfirstlane(k_x % a.n_kv_heads);
     const int unit = __builtin_amdgcn_readfirstlane((k_x / a.n_kv_heads) * 8 + (blockIdx.x & 7));
     if (unit >= a.n_units) return;
-    const int chunk = __builtin_amdgcn_readfirstlane(unit % a.max_chunks);
-    const int rest = __builtin_amdgcn_readfirstlane(unit / a.max_chunks);
+    const int chunk = __builtin_amdgcn_readfirstlane(unit / a.seq_units);
+    const int rest = __builtin_amdgcn_readfirstlane(unit - chunk * a.seq_units);
     const int qb = __builtin_amdgcn_readfirstlane(rest % a.q_blocks);
     const int b = __builtin_amdgcn_readfirstlane(rest / a.q_blocks);
     const int t_begin = chunk * a.chunk_tiles;
@@ -1032,6 +1036,7 @@ int hd_launch(const void* query, const void* k_data, const void* v_data, const v
     a.group = (int)g;
     a.q_blocks = (int)q_blocks;
     a.n_units = (int)units;
+    a.seq_units = (int)(batch * q_blocks);
     a.max_chunks = max_chunks;
     a.chunk_tiles = chunk_tiles;
     a.max_pages = (int)max_pages;

@@ -214,26 +214,33 @@ def pages_workspace(B, Hq, D, max_chunks, balanced=False):
             + r(s2 * Hq * D * 4) + r(s2 * Hq * 2 * 4))
 
 
-@pytest.mark.parametrize("cfg,expect_chunks,expect_pages", [
+@pytest.mark.parametrize("cfg,expect_chunks,kernel", [
     # (B, Hq, Hkv, D, maxP, total, max)
-    ((32, 32, 8, 128, 256, 32 * 4096, 4096), True, True),      # Llama-3-8B shape: page kernel
-    ((64, 32, 8, 128, 1024, 64 * 3000, 16384), True, True),    # ragged batch: page kernel, balanced mode
-    ((4, 64, 8, 128, 8192, 4 * 131072, 131072), True, True),   # 8 query heads per kv head: streaming kernel
-    ((4, 8, 2, 64, 16, 400, 200), False, False),               # D = 64: general; tiny grid, one chunk
-    ((8, 32, 8, 128, 512, 8 * 8192, 8192), True, False),       # 75 MB of K/V: general kernel
+    ((32, 32, 8, 128, 256, 32 * 4096, 4096), True, "pages"),      # Llama-3-8B shape: page kernel
+    ((64, 32, 8, 128, 1024, 64 * 3000, 16384), True, "pages"),    # ragged batch: page kernel, balanced mode
+    ((4, 64, 8, 128, 8192, 4 * 131072, 131072), True, "pages"),   # 8 query heads per kv head: streaming kernel
+    ((4, 8, 2, 64, 16, 400, 200), False, "general"),              # D = 64: general; tiny grid, one chunk
+    ((8, 32, 8, 128, 512, 8 * 8192, 8192), True, "hd"),           # 75 MB of K/V: head-dim kernel, token pages
+    ((64, 32, 8, 128, 64, 64 * 1024, 1024), True, "general"),     # 512 units: general kernel
+    ((64, 32, 8, 128, 256, 64 * 1000, 4096), True, "general"),    # ragged: general kernel
 ])
-def test_decode_plan_covers_every_tile(cfg, expect_chunks, expect_pages):
+def test_decode_plan_covers_every_tile(cfg, expect_chunks, kernel):
     B, Hq, Hkv, D, maxP, total, mx = cfg
     chunk_tiles, max_chunks, nw, ws = decode_plan(B, Hq, Hkv, D, maxP, total, mx)
     if chunk_tiles < 0:  # the balanced mode (test_balanced_plan_for_ragged_lengths)
-        assert expect_pages and nw == 16 and -chunk_tiles <= 64
+        assert kernel == "pages" and nw == 16 and -chunk_tiles <= 64
         assert ws == pages_workspace(B, Hq, D, max_chunks, balanced=True)
         return
     tiles = (maxP * 16 + 31) // 32
     assert chunk_tiles * max_chunks >= tiles
     assert (chunk_tiles * (max_chunks - 1)) < tiles
-    assert (nw == 16) == expect_pages and (nw == 16 or 1 <= nw <= 4)
     assert (max_chunks > 1) == expect_chunks
+    if kernel == "hd":
+        w = 16 if D == 64 else 8
+        assert nw == w | 0x800 and chunk_tiles % w == 0 and chunk_tiles <= 32 * w
+        assert ws == (any_workspace(B, Hq, D, max_chunks) if max_chunks > 1 else 0)
+        return
+    assert (nw == 16) == (kernel == "pages") and (nw == 16 or 1 <= nw <= 4)
     assert chunk_tiles <= 64  # a chunk's page ids fit two VGPRs
     if max_chunks == 1:
         assert ws == 0
@@ -248,7 +255,8 @@ def test_gqa8_plans():
     # chunk mode only, so 16-wave requests get chunk plans even for ragged
     # lengths; the page-kernel bit keeps the page kernel's balanced mode; a
     # block table wider than 64 chunks of 64 tiles leaves the plan's choice to
-    # the general kernel; a short batch too.
+    # the general kernel; a short batch goes to the head-dim kernel's
+    # token-page mode, a shorter one to the general kernel.
     B, Hq, Hkv, D = 4, 64, 8, 128
     ct, mc, nw, ws = decode_plan(B, Hq, Hkv, D, 8192, B * 131072, 131072)
     assert (ct, mc, nw) == (64, 64, 16) and ws == pages_workspace(B, Hq, D, 64)
@@ -258,7 +266,11 @@ def test_gqa8_plans():
                                 waves_per_block=16 | DECODE_PAGE_KERNEL)
     assert ct < 0 and nw == 16 | DECODE_PAGE_KERNEL
     assert decode_plan(B, Hq, Hkv, D, 8193, B * 131072, 131072)[2] <= 4
-    assert decode_plan(B, Hq, Hkv, D, 64, B * 1024, 1024)[2] <= 4
+    assert decode_plan(1, Hq, Hkv, D, 8192, 131072, 131072)[2] <= 4   # one or two sequences: the general kernel
+    assert decode_plan(2, Hq, Hkv, D, 8192, 2 * 131072, 131072)[2] <= 4
+    assert decode_plan(3, Hq, Hkv, D, 4096, 3 * 65536, 65536)[2] == 16
+    assert decode_plan(B, Hq, Hkv, D, 64, B * 1024, 1024)[2] == 8 | 0x800  # 4.7 MB: the head-dim kernel
+    assert decode_plan(B, Hq, Hkv, D, 64, B * 512, 512)[2] <= 4             # 2.4 MB: the general kernel
 
 
 @pytest.mark.parametrize("cfg", [
