@@ -125,7 +125,9 @@ int iris_quantize_pack_int4(const void *x, void *packed, void *scales, int64_t n
  * tokens_per_split > 0 and waves_per_block > 0 override the heuristic:
  * its low 8 bits ask for a wave count (16: a page-streaming kernel; 1-4:
  * the general kernel; head_dim 96, 160, 192 and 224 have a kernel of their
- * own whose wave count, 12 or 8, the plan sets), and one of the selection
+ * own whose wave count, 12 or 8, the plan sets; at head_dim 64 and 128 the
+ * plan may return that kernel's token-page mode, 16 or 8 waves with
+ * IRIS_DECODE_TOKEN_PAGES), and one of the selection
  * bits below may be or-ed in.  out_waves carries the wave count and the
  * selection bit into the launch, so a plan and its launch always run the
  * same kernel.

@@ -1,22 +1,26 @@
 // INT4 paged decode attention for gfx950 (MI355X): the MFMA kernel for the
-// head dims between the fast kernels' 64, 128 and 256.
+// head dims between the fast kernels' 64, 128 and 256, and, in its
+// token-page mode, for every page size.
 //
 // Replaces the TileLang kernel `_int4_paged_decode_attention`
 // (src/iris_kernel/fused_attention.py:11-220 in Hunter2030ZeRo/Iris-Kernel)
 // for head_dim 96, 160, 192 and 224 (G = 3, 5, 6, 7 scale groups of 32
 // dims), any number of kv heads and of query heads per kv head, pages of
-// 16 m tokens; it computes the result of
+// 16 m tokens; in token-page mode (TOK) for head_dim 64 to 224 (G = 2-7)
+// where G x Hkv is even and pages of any size, each token's page looked up
+// through the block table.  It computes the result of
 // `torch_eager_int4_paged_decode_attention`
 // (src/iris_kernel/torch_eager_attention.py:154-239), which takes any head
-// dim that is a multiple of the group size (:93) where the reference's fused
-// path takes 64 and 128 (fused_attention.py:390-403).
+// dim that is a multiple of the group size (:93) and any page size (:72)
+// where the reference's fused path takes 64 and 128 and pages of 16
+// (fused_attention.py:390-403).
 //
-// Streaming: a workgroup of W waves (12 at G = 3, 8 above) owns (sequence,
+// Streaming: a workgroup of W waves (16 at G = 2, 12 at 3, 8 above) owns (sequence,
 // kv head, block of up to 16 of its query heads, chunk of 32-token tiles);
 // the kv heads of one (sequence, query block, chunk) run on one XCD, one
 // after another, so the cache lines their rows share are fetched into one
 // L2.  Wave w streams tiles w, w + W, ... of the chunk through R LDS slots
-// of its own (three at G = 3 and 5, two above), with no workgroup barrier in
+// of its own (three at G = 3 to 5, two at 2, 6 and 7), with no workgroup barrier in
 // the loop.  Per tile a wave
 // * issues the loads of the tile R - 1 ahead into the slot the previous
 //   tile used, waits for this tile's (vmcnt) and computes it, reading the
@@ -28,7 +32,10 @@
 //   pieces token-major) and, per token, the aligned dwords that cover its
 //   2 G bytes of each scale tensor (a kv head's scales start on an odd half
 //   when kv head * G or the row is odd; the dword count covers the shift);
-// * keeps its page ids in lanes of one register (v_readlane).
+// * keeps its page ids in lanes of one register (v_readlane); in token-page
+//   mode it loads the block-table entries of a tile's 32 tokens into LDS one
+//   tile ahead of the data, and each load lane takes its token's slot in the
+//   pool with ds_bpermute.
 //
 // Compute, the query heads of the block as the 16 MFMA columns
 // (v_mfma_f32_16x16x32_f16):
