@@ -146,6 +146,16 @@ __device__ __forceinline__ int virtual_page(const int32_t* row, int vp, int page
     return row[e] * m + (vp - e * m);
 }
 
+// Grids whose slowest index is the split-KV chunk c (each XCD -- workgroup
+// i runs on XCD i % 8 -- then gets its share of every chunk index, and the
+// chunks past the sequences' ends leave no XCD idle) rotate the index r of
+// the n sequences (or units) of a chunk by c, so one sequence's chunks run on
+// different XCDs: position p of chunk c holds r = (p - c) mod n.
+__device__ __forceinline__ int rotate_back(int p, int c, int n) {
+    const int r = p - c % n;
+    return r < 0 ? r + n : r;
+}
+
 // LDS a workgroup may use on gfx950 (per CU).
 constexpr int kMaxLdsBytes = 160 * 1024;
 

@@ -1484,11 +1484,12 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
     // head_dim 96, 160, 192 and 224: the MFMA kernel of decode_hd.hip
     // (page sizes of 16 m tokens; the others ask for the any-shape kernel).
     if (sel == 0 && hd_supported(head_dim))
-        return hd_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, max_tokens, tokens_per_split, false,
-                       out_chunk_tiles, out_max_chunks, out_waves, out_workspace_bytes);
+        return hd_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, total_tokens, max_tokens,
+                       tokens_per_split, false, out_chunk_tiles, out_max_chunks, out_waves, out_workspace_bytes);
     if (sel == kTokenPages && hd_tok_supported(head_dim, num_kv_heads)) {
-        const int st = hd_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, max_tokens, tokens_per_split,
-                               true, out_chunk_tiles, out_max_chunks, out_waves, out_workspace_bytes);
+        const int st = hd_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, total_tokens, max_tokens,
+                               tokens_per_split, true, out_chunk_tiles, out_max_chunks, out_waves,
+                               out_workspace_bytes);
         if (st == kOk) *out_waves |= kTokenPages;
         return st;
     }
@@ -1519,8 +1520,9 @@ extern "C" int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_
     }
     if (sel == 0 && waves_of(waves_per_block) == 0 &&
         hd_preferred(batch, num_q_heads, num_kv_heads, head_dim, est_total, est_max)) {
-        const int st = hd_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, max_tokens, tokens_per_split,
-                               true, out_chunk_tiles, out_max_chunks, out_waves, out_workspace_bytes);
+        const int st = hd_plan(batch, num_q_heads, num_kv_heads, head_dim, max_pages, total_tokens, max_tokens,
+                               tokens_per_split, true, out_chunk_tiles, out_max_chunks, out_waves,
+                               out_workspace_bytes);
         if (st == kOk) *out_waves |= kTokenPages;
         return st;
     }

@@ -109,17 +109,15 @@ __global__ __launch_bounds__(kThreads) void int4_decode_any_kernel(Args a) {
     float* const p_s = reinterpret_cast<float*>(smem + L.p);
     const int SK = kc_row(G);
 
-    // ---- (chunk, sequence, kv head, query block), chunks slowest: each XCD
-    // (workgroup i runs on XCD i % 8) gets its share of every chunk index,
-    // so chunks past the sequences' ends, which return at once, leave no
-    // XCD idle
+    // ---- (chunk, sequence, kv head, query block), chunks slowest, the
+    // sequences rotated by the chunk (rotate_back in common.h)
     int rest = blockIdx.x;
     const int qb = rest % a.q_blocks;
     rest /= a.q_blocks;
     const int kvh = rest % a.n_kv_heads;
     rest /= a.n_kv_heads;
-    const int b = rest % a.batch;
     const int chunk = rest / a.batch;
+    const int b = rotate_back(rest % a.batch, chunk, a.batch);
     const int seq_len = a.seq_lens[b];
     const int64_t t_begin64 = (int64_t)chunk * a.chunk_tok;
     if (t_begin64 >= seq_len) return;  // uniform: this chunk holds no token

@@ -128,14 +128,12 @@ void fp16_decode_kernel(Args a) {
 
     // kv head fastest: the Hkv workgroups of a chunk read their slices of
     // the same pages side by side (MI355X, B=32, L=4096: 120.9 us against
-    // 122.8 with the chunks of one head adjacent); chunk slowest, so each
-    // XCD (workgroup i runs on XCD i % 8) gets its share of every chunk
-    // index and chunks past the sequences' ends, which return at once, leave
-    // no XCD idle.
+    // 122.8 with the chunks of one head adjacent); chunk slowest, sequences
+    // rotated by the chunk (rotate_back in common.h).
     const int wg = blockIdx.x;
     const int j = wg % a.n_kv_heads;
-    const int b = (wg / a.n_kv_heads) % a.batch;
     const int chunk = wg / a.n_kv_heads / a.batch;
+    const int b = rotate_back((wg / a.n_kv_heads) % a.batch, chunk, a.batch);
     const int bj = b * a.n_kv_heads + j;
     const int g = a.group;
 

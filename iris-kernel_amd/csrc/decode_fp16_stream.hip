@@ -197,11 +197,9 @@ __global__ __launch_bounds__(1024) void fp16_decode_stream_kernel(const int32_t*
     const int rowb = cpr * 16;          // bytes of a token row
     const int g = a.group;
 
-    // chunk slowest (the grid is batch x max_chunks): each XCD (workgroup i
-    // runs on XCD i % 8) gets its share of every chunk index, so chunks past
-    // the sequences' ends, which return at once, leave no XCD idle
+    // chunk slowest, sequences rotated by the chunk (rotate_back in common.h)
     const int batch = gridDim.x / p_max_chunks;
-    const int chunk = blockIdx.x / batch, b = blockIdx.x - chunk * batch;
+    const int chunk = blockIdx.x / batch, b = rotate_back(blockIdx.x - chunk * batch, chunk, batch);
     const int p0 = chunk * p_chunk_pages;
     const int32_t* bt = p_block_table + (int64_t)b * p_max_pages;
     // page ids of the chunk: logical page p0 + i in lane i of pid0 / pid1

@@ -19,13 +19,14 @@ IRIS_INTERNAL bool hd_tok_supported(int64_t head_dim, int64_t num_kv_heads);
 // Waves of the kernel's workgroups at head_dim (16 at 64, 12 at 96, 8 above).
 IRIS_INTERNAL int hd_waves(int64_t head_dim);
 
-// Chunk plan: chunk_tiles (a multiple of the waves, at most 120 or 128 32-token
-// tiles) and max_chunks for a grid of about one workgroup per CU over the
-// (sequence, kv head, block of 16 query heads) units; workspace bytes for
-// the split.  max_pages counts the 16-token pages a table row addresses
+// Chunk plan: chunk_tiles (a multiple of the waves, at most 32 tiles of 32
+// tokens a wave) and max_chunks, a chunk about one CU's share of the tiles of
+// the (sequence, kv head, block of 16 query heads) units; workspace bytes for
+// the split.  total_tokens / max_tokens may be -1 (unknown).  max_pages counts the 16-token pages a table row addresses
 // (rounded up in token-page mode).
 IRIS_INTERNAL int hd_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
-                          int64_t max_pages, int64_t max_tokens, int32_t tokens_per_split, bool token_pages,
+                          int64_t max_pages, int64_t total_tokens, int64_t max_tokens, int32_t tokens_per_split,
+                          bool token_pages,
                           int32_t* out_chunk_tiles, int32_t* out_max_chunks, int32_t* out_waves,
                           int64_t* out_workspace_bytes);
 

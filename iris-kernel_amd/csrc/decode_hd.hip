@@ -387,7 +387,10 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     // cache lines they share are fetched into one L2.  With the chunk index
     // slowest, each XCD gets its share of every chunk index (chunks past a
     // sequence's end, which return at once, would otherwise leave whole XCDs
-    // idle when the table is wider than the sequences).  The grid is padded
+    // idle when the table is wider than the sequences); within chunk c the
+    // (sequence, query block) index is rotated by c, so a sequence's chunks
+    // run on different XCDs (a long sequence of a ragged batch would
+    // otherwise load one XCD's share of the bandwidth).  The grid is padded
     // to whole groups of 8 units; padding workgroups return at once.  The
     // divisions run on the VALU; readfirstlane keeps the results, and all
     // that derives from them (the loop bounds among it), scalar.
@@ -396,7 +399,7 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     const int unit = __builtin_amdgcn_readfirstlane((k_x / a.n_kv_heads) * 8 + (blockIdx.x & 7));
     if (unit >= a.n_units) return;
     const int chunk = __builtin_amdgcn_readfirstlane(unit / a.seq_units);
-    const int rest = __builtin_amdgcn_readfirstlane(unit - chunk * a.seq_units);
+    const int rest = __builtin_amdgcn_readfirstlane(rotate_back(unit - chunk * a.seq_units, chunk, a.seq_units));
     const int qb = __builtin_amdgcn_readfirstlane(rest % a.q_blocks);
     const int b = __builtin_amdgcn_readfirstlane(rest / a.q_blocks);
     const int t_begin = chunk * a.chunk_tiles;
@@ -950,8 +953,8 @@ static int64_t hd_workspace_bytes(int64_t batch, int64_t num_q_heads, int64_t he
 }
 
 int hd_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t max_pages,
-            int64_t max_tokens, int32_t tokens_per_split, bool token_pages, int32_t* out_chunk_tiles,
-            int32_t* out_max_chunks, int32_t* out_waves, int64_t* out_workspace_bytes) {
+            int64_t total_tokens, int64_t max_tokens, int32_t tokens_per_split, bool token_pages,
+            int32_t* out_chunk_tiles, int32_t* out_max_chunks, int32_t* out_waves, int64_t* out_workspace_bytes) {
     const bool ok = token_pages ? hd_tok_supported(head_dim, num_kv_heads) : hd_supported(head_dim);
     if (!ok || batch <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads != 0 || max_pages <= 0)
         return kInvalidArgument;
@@ -959,18 +962,32 @@ int hd_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t he
     const int W = hd_waves(head_dim);
     const int64_t cap_tokens = max_pages * 16;
     if (max_tokens < 0 || max_tokens > cap_tokens) max_tokens = cap_tokens;
+    if (total_tokens < 0 || total_tokens > batch * max_tokens) total_tokens = batch * max_tokens;
     // The grid covers every tile block_table can address; the lengths steer
-    // the chunk size: about one workgroup a CU (256 on MI355X) over the
-    // (sequence, kv head, query block) units, in whole steps of W tiles.
+    // the chunk size: one CU's share (256 CUs on MI355X) of the tiles of all
+    // (sequence, kv head, query block) units, so that no workgroup holds
+    // more than its CU's share (a ragged batch's long sequences are split,
+    // the short ones take one chunk each; the tiles of a batch: about
+    // total / 32 + batch / 2, at most batch x the longest); but no less than
+    // the longest sequence over the units a CU gets, up to 8 tiles a wave
+    // (below that a workgroup's fixed costs, and the split's, outweigh the
+    // balance: MI355X, B=128, Hq=16, Hkv=1, D=96, lengths in [128, 8192]:
+    // 39.6 us with chunks of 3 tiles a wave against 34.2 with 11).
     const int64_t max_tiles = (cap_tokens + hd::kTile - 1) / hd::kTile;
     const int64_t longest = (max_tokens + hd::kTile - 1) / hd::kTile;
     int64_t chunk_tiles;
     if (tokens_per_split > 0) {
         chunk_tiles = (tokens_per_split + hd::kTile - 1) / hd::kTile;
     } else {
+        int64_t tiles = total_tokens / hd::kTile + batch / 2;
+        if (tiles > batch * longest) tiles = batch * longest;
+        const int64_t share = (tiles * num_kv_heads * q_blocks + 255) / 256;
         int64_t per_unit = 256 / (batch * num_kv_heads * q_blocks);
         if (per_unit < 1) per_unit = 1;
-        chunk_tiles = (longest + per_unit - 1) / per_unit;
+        int64_t floor_tiles = (longest + per_unit - 1) / per_unit;
+        if (floor_tiles > 8 * W) floor_tiles = 8 * W;
+        chunk_tiles = share > floor_tiles ? share : floor_tiles;
+        if (chunk_tiles > longest) chunk_tiles = longest;
     }
     const int64_t cap = hd_max_chunk_tiles(W);
     chunk_tiles = (chunk_tiles + W - 1) / W * W;

@@ -217,11 +217,9 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_mqa_kernel(
     const int n = lane & 15;   // MFMA row (A) or column (B, C): token or query head
     const int jq = lane >> 4;  // MFMA k-chunk (A, B) or row quad (C)
 
-    // chunk slowest (the grid is batch x max_chunks): each XCD (workgroup i
-    // runs on XCD i % 8) gets its share of every chunk index, so chunks past
-    // the sequences' ends, which return at once, leave no XCD idle
+    // chunk slowest, sequences rotated by the chunk (rotate_back in common.h)
     const int batch = gridDim.x / p_max_chunks;
-    const int chunk = blockIdx.x / batch, b = blockIdx.x - chunk * batch;
+    const int chunk = blockIdx.x / batch, b = rotate_back(blockIdx.x - chunk * batch, chunk, batch);
     const int t_begin = chunk * p_chunk_tiles;
     const int p0 = 2 * t_begin;  // first 16-token page of the chunk
     const int32_t* bt = p_block_table + (int64_t)b * p_bt_cols;
