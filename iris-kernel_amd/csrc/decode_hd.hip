@@ -19,11 +19,10 @@
 // kv head, block of up to 16 of its query heads, chunk of 32-token tiles);
 // the kv heads of one (sequence, query block, chunk) run on one XCD, one
 // after another, so the cache lines their rows share are fetched into one
-// L2.  Wave w streams tiles w, w + W, ... of the chunk through R LDS slots
-// of its own (three at G = 3 to 5, two at 2, 6 and 7), with no workgroup barrier in
-// the loop.  Per tile a wave
-// * issues the loads of the tile R - 1 ahead into the slot the previous
-//   tile used, waits for this tile's (vmcnt) and computes it, reading the
+// L2.  Wave w streams tiles w, w + W, ... of the chunk through two LDS slots
+// of its own, with no workgroup barrier in the loop.  Per tile a wave
+// * issues the loads of the next tile into the slot the previous tile
+//   used, waits for this tile's (vmcnt) and computes it, reading the
 //   slot in two phases (K codes and scales before QK, V codes and scales
 //   before PV) so that only half of a tile's operands are live in registers
 //   at once;
@@ -71,9 +70,9 @@ typedef int int2v_t __attribute__((ext_vector_type(2)));
 template <int G_>
 struct Geo {
     static constexpr int G = G_, D = 32 * G_, HB = 16 * G_;  // groups, head_dim, code bytes of a head row
-    // waves a workgroup and LDS slots a wave (R - 1 tiles in flight while one is computed)
+    // waves a workgroup and LDS slots a wave (one tile in flight while one is computed)
     static constexpr int W = G_ <= 2 ? 16 : G_ <= 3 ? 12 : 8;
-    static constexpr int R = G_ <= 2 ? 2 : G_ <= 5 ? 3 : 2;
+    static constexpr int R = 2;
     static constexpr int NK = (32 * G_ + 63) / 64;  // 16-byte loads a tensor a tile
     static constexpr int KA = 512 * G_;             // code area of a slot, per tensor (32 G pieces)
     static constexpr int SD = G_ / 2 + 1;                    // scale dwords a token needs (at most)
@@ -93,7 +92,7 @@ struct Geo {
     static constexpr int ID_OFF = (MAIN_BYTES + 15) / 16 * 16, ID_BYTES = 2 * 32 * 4;
     static constexpr int LDS_BYTES = MAIN_BYTES;
     static constexpr int LDS_BYTES_TOK = ID_OFF + W * ID_BYTES;
-    static_assert(R >= 2 && R <= 3, "ring depth");
+    static_assert(R == 2, "ring depth (the pipeline alternates two slots)");
     static_assert(NA <= SP && SD <= SP, "scale dwords of a token");
     static_assert(LDS_BYTES_TOK <= 160 * 1024, "LDS of a CU");
 };
@@ -505,11 +504,6 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
             }
         }
     };
-    if constexpr (!TOK) {
-#pragma unroll
-        for (int s = 0; s < L::R - 1; ++s)
-            if (s < n_my) issue(s, s);
-    }
 
     // ---- token-page mode: a tile's 32 tokens (the last valid one for those
     // past the sequence) are looked up one by one.  Lane l < 32 loads the
@@ -725,75 +719,52 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
         }
     };
 
-    // ---- the pipeline, per wave (no workgroup barrier): tile s is computed
-    // once this wave's loads of it have landed (vmcnt counts in order; every
-    // load instruction of a tile has a lane that issues it, so a tile is
-    // always JOBS of them), with tiles s + 1 .. s + R - 1 in flight; slot
-    // (s - 1) % R, whose reads by tile s - 1 have returned, receives tile
-    // s + R - 1 first.
+    // ---- the pipeline, per wave (no workgroup barrier), two LDS slots: tile
+    // s is computed from slot s & 1 once this wave's loads of it have landed
+    // (vmcnt counts in order; every load instruction of a tile has a lane
+    // that issues it, so a tile is always JOBS of them), with tile s + 1 in
+    // flight into the other slot, whose reads by tile s - 1 have returned.
+    // (Three slots, two tiles in flight, measured 1-7% slower at G = 3, 4
+    // and 5 on MI355X.)
     //
-    // Token-page mode: per tile one more load (its block-table entries), the
-    // entries one tile ahead of the data: iteration s reads the entries of
-    // tile s + R - 1 (loaded at s - 1, before the data of tile s + R - 2),
-    // issues the entries of tile s + R, then the data of tile s + R - 1.
-    constexpr int R = L::R;
+    // Token-page mode: per tile one more load (its block-table entries), one
+    // tile ahead of the data: iteration s reads the entries of tile s + 1
+    // (loaded at s - 1, before the data of tile s), issues the entries of
+    // tile s + 2, then the data of tile s + 1.
     constexpr int JOBS = 2 * NK + 2 * NS;
-    static_assert((R - 1) * JOBS + 2 < 64, "vmcnt range");
+    static_assert(JOBS + 2 < 64, "vmcnt range");
     const uint32_t ring_addr = lds_addr(ring);
-    int slot_c = 0;          // slot of tile s
-    int slot_i = R - 1;      // slot of tile s + R - 1
     if constexpr (TOK) {
-        // entries of tiles 0 and 1, then data 0, (R = 3: entries 2,) data 1
+        // entries of tiles 0 and 1, then the data of tile 0
         if (n_my > 0) issue_entries(0);
         if (n_my > 1) issue_entries(1);
         wait_vmcnt<0>();
         if (n_my > 0) issue_tok(0, slots_of(0));
-        if constexpr (R == 3) {
-            if (n_my > 2) issue_entries(2);
-            if (n_my > 1) issue_tok(1, slots_of(1));
-        }
+    } else {
+        if (n_my > 0) issue(0, 0);
     }
     for (int s = 0; s < n_my; ++s) {
-        const int ahead = min(n_my - 1 - s, R - 1);  // tiles in flight behind tile s
-        if constexpr (!TOK) {
-            if (ahead == R - 1) {
-                issue(s + R - 1, slot_i);
-                wait_vmcnt<(R - 1) * JOBS>();
-            } else if (R > 2 && ahead == 1) {
-                wait_vmcnt<JOBS>();
-            } else {
-                wait_vmcnt<0>();
-            }
-        } else if constexpr (R == 2) {
-            if (ahead == 1) {
-                wait_vmcnt<JOBS>();  // the entries of tile s + 1 (tile s's data may fly)
-                const int sl = slots_of(s + 1);
-                if (s + 2 < n_my) {
-                    issue_entries(s + 2);
-                    issue_tok(slot_i, sl);
-                    wait_vmcnt<JOBS + 1>();  // tile s
-                } else {
-                    issue_tok(slot_i, sl);
-                    wait_vmcnt<JOBS>();
-                }
-            } else {
-                wait_vmcnt<0>();
-            }
-        } else {
-            if (ahead == 2) {
-                wait_vmcnt<JOBS>();  // tile s and the entries of tile s + 2 (tile s + 1 flies)
-                const int sl = slots_of(s + 2);
-                if (s + 3 < n_my) issue_entries(s + 3);
-                issue_tok(slot_i, sl);
-            } else if (ahead == 1) {
+        const int next = (s + 1) & 1;  // slot of tile s + 1
+        if (s + 1 < n_my) {
+            if constexpr (!TOK) {
+                issue(s + 1, next);
                 wait_vmcnt<JOBS>();  // tile s
             } else {
-                wait_vmcnt<0>();
+                wait_vmcnt<JOBS>();  // the entries of tile s + 1 (tile s's data may fly)
+                const uint32_t sl = slots_of(s + 1);
+                if (s + 2 < n_my) {
+                    issue_entries(s + 2);
+                    issue_tok(next, sl);
+                    wait_vmcnt<JOBS + 1>();  // tile s
+                } else {
+                    issue_tok(next, sl);
+                    wait_vmcnt<JOBS>();  // tile s
+                }
             }
+        } else {
+            wait_vmcnt<0>();
         }
-        compute(t_begin + W * s + wave, ring_addr + (uint32_t)(slot_c * SLOT));
-        slot_c = slot_c == R - 1 ? 0 : slot_c + 1;
-        slot_i = slot_i == R - 1 ? 0 : slot_i + 1;
+        compute(t_begin + W * s + wave, ring_addr + (uint32_t)((s & 1) * SLOT));
     }
     wait_vmcnt<0>();
     __syncthreads();

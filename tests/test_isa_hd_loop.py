@@ -2,11 +2,11 @@
 gfx950 code (csrc/decode_hd.hip, every G instance of both modes: pages of
 16 m tokens, and token pages at head_dim 64-224).
 
-A wave keeps R - 1 tiles' direct-to-LDS loads in flight while it computes
-one, which holds only if every vmcnt wait in the loop is one of the kernel's
-own (a multiple of one tile's load instructions, plus, in token-page mode,
-the one load of a tile's block-table entries: the compiler would otherwise
-wait for the loads streaming into the other slots).  Two
+A wave keeps the next tile's direct-to-LDS loads in flight while it
+computes one, which holds only if every vmcnt wait in the loop is one of the
+kernel's own (one tile's load instructions or none, plus, in token-page
+mode, the one load of a tile's block-table entries: the compiler would
+otherwise wait for the loads streaming into the other slot).  Two
 regressions this guards against, both seen while the kernel was written: the
 loop compiled as a divergent loop (its bounds in VGPRs, an exec-mask exit
 around every tile), and spilled registers.  Compiles decode_hd.hip once
@@ -83,7 +83,9 @@ def test_tile_loop_waits_only_for_its_own_tiles(asm, g, tok):
     jobs = jobs_of(g)
     loads = sum(1 for l in loop if l.startswith("global_load_lds"))
     waits = {int(m) for l in loop if l.startswith("s_waitcnt") for m in re.findall(r"vmcnt\((\d+)\)", l)}
-    assert 0 in waits and len(waits) >= 2, waits
+    # one tile in flight while one is computed (the last tile's vmcnt(0) may
+    # sit in the loop or in its peeled last iteration)
+    assert jobs in waits, (jobs, sorted(waits))
     if not tok:
         assert loads == jobs, (loads, jobs)  # one tile's loads, issued once a step
         assert all(w % jobs == 0 and w < 64 for w in waits), (jobs, sorted(waits))
