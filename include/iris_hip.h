@@ -160,7 +160,8 @@ int iris_quantize_pack_int4(const void *x, void *packed, void *scales, int64_t n
  * iris_decode_plan returns the any-shape kernel's plan (out_waves then
  * carries IRIS_DECODE_ANY_KERNEL).  It is the bit to ask for when the page
  * size is not a multiple of 16 up to 256; it may be asked for at any page
- * size. */
+ * size.  The mode addresses token slots (page id x page_size + offset) in
+ * 32 bits: a pool of at most 2^32 token slots. */
 #define IRIS_DECODE_TOKEN_PAGES 0x800
 int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                      int64_t max_pages, int64_t total_tokens, int64_t max_tokens,

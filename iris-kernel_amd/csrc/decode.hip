@@ -1588,7 +1588,6 @@ extern "C" int iris_int4_paged_decode_attention(
     int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_size,
     int64_t num_pages, int64_t max_pages, float softmax_scale, int32_t chunk_tiles,
     int32_t max_chunks, int32_t waves_per_block, void* stream) {
-    (void)num_pages;
     const int32_t sel = selection_of(waves_per_block);
     if (sel < 0) return kInvalidArgument;
     if (sel == kAnyKernel)
@@ -1596,7 +1595,10 @@ extern "C" int iris_int4_paged_decode_attention(
                           workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, page_size,
                           max_pages, softmax_scale, chunk_tiles, max_chunks, stream);
     if (sel == kTokenPages) {
-        if (page_size < 1 || max_pages <= 0 || page_size > 0x3FFFFFFF || max_pages > 0x3FFFFFFF)
+        // token slots in 32 bits (2^32 slots of the smallest row, 72 bytes at
+        // one kv head and head_dim 64, are more than an MI355X's 288 GB)
+        if (page_size < 1 || max_pages <= 0 || page_size > 0x3FFFFFFF || max_pages > 0x3FFFFFFF ||
+            num_pages < 0 || num_pages > ((int64_t)1 << 32) || num_pages * page_size > ((int64_t)1 << 32))
             return kInvalidArgument;
         const int64_t pages16 = (max_pages * page_size + kPageSize - 1) / kPageSize;
         return hd_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,

@@ -104,6 +104,7 @@ def test_decode_rejects_unsupported_shapes_before_launch():
     assert call(D=96, P=0, nw=12 | tok, ct=12, mc=1) == 1   # page_size >= 1
     assert call(D=96, P=200, nw=12 | tok, ct=12, mc=2) == 1  # chunks do not cover 4 x 200 tokens
     assert call(D=96, P=200, nw=12 | tok, ct=24, mc=2) == 3  # two chunks need a workspace
+    assert call(D=96, P=2, NP=(1 << 31) + 1, nw=12 | tok, ct=12, mc=1) == 1  # token slots in 32 bits
     assert call(Hq=9) == 1          # Hq not divisible by Hkv
     assert call(ct=1, mc=1) == 1    # chunks do not cover max_pages
     assert call(nw=5) == 1
