@@ -101,6 +101,19 @@ def test_noalloc_head_dim_and_any_shape_kernels_two_calls(device):
              waves=0x400)
 
 
+def test_noalloc_token_pages_two_calls(device):
+    """The head-dim kernel's token-page mode (asked for at head_dim 128 and
+    64, 16-token pages), each larger call then smaller."""
+    one_call(device, batch=8, max_pages=128, max_len=2048, tokens_per_split=256, seed=41, hq=32, hkv=8, d=128,
+             waves=0x800)
+    one_call(device, batch=3, max_pages=64, max_len=900, tokens_per_split=128, seed=42, hq=32, hkv=8, d=128,
+             waves=0x800)
+    one_call(device, batch=6, max_pages=96, max_len=1536, tokens_per_split=256, seed=43, hq=16, hkv=1, d=64,
+             waves=0x800)
+    one_call(device, batch=2, max_pages=64, max_len=900, tokens_per_split=128, seed=44, hq=16, hkv=1, d=64,
+             waves=0x800)
+
+
 def test_noalloc_rejects_plan_beyond_scratch(device):
     batch, hq, hkv, d, max_pages = 64, 32, 8, 128, 256
     plan = decode_plan(batch, hq, hkv, d, max_pages, batch * max_pages * 16, max_pages * 16, 64, 0)
