@@ -1446,25 +1446,27 @@ static bool mqa_preferred(int64_t batch, int64_t total_tokens, int64_t max_token
     return 4 * total_tokens >= 3 * batch * max_tokens;
 }
 
-// head_dim 64 and 128 at mid sizes: the head-dim kernel (decode_hd.hip) in
-// its token-page mode takes the shapes the plan would give the general
-// kernel when they read between kHdMinBytes and kPagesMinBytes of K/V over
-// batches of similar lengths in at most 256 (sequence, kv head, query block)
-// units -- its W-wave workgroups stream a unit's tiles with no workgroup
-// barrier and its grid follows the XCDs (MI355X, interleaved: B=4, L=8192,
-// Hkv=8: 22.6 against 25.5 us; B=32, L=2048: 29.7 against 33.1; D=64,
-// Hq=32, Hkv=8, B=32, L=2048: 20.8 against 25.8; B=1, L=32768: 26.1 against
-// 49.9).  Smaller launches are latency-bound and come out even or slower,
-// and more units (B=64, L=1024: 34.9 against 33.0) or ragged lengths (B=64,
-// lengths in [16, 4096]: 51.3 against 43.1) favour the general kernel's
-// smaller workgroups.
+// head_dim 64 and 128 below kPagesMinBytes: the head-dim kernel
+// (decode_hd.hip) in its token-page mode takes the shapes the plan would
+// give the general kernel when they have at least two kv heads, lengths of
+// similar size and at most 256 (sequence, kv head, query block) units, and
+// read at least kHdMinBytes of K/V at head_dim 64 -- its W-wave workgroups
+// stream a unit's tiles with no workgroup barrier and its grid follows the
+// XCDs (MI355X, back-to-back launches, us: B=4, L=8192, Hkv=8: 19.3 against
+// 21.8; B=32, L=2048: 25.7 against 30.4; D=64, Hq=32, Hkv=8, B=32, L=2048:
+// 16.8 against 21.8; B=1, L=32768: 22.5 against 47.2; B=1, Hq=32, Hkv=8,
+// L=128: 7.3 against 8.2).  At head_dim 64 smaller launches favour the
+// general kernel (B=1, Hq=32, Hkv=8, L=1024: 9.9 against 9.1), as do one kv
+// head (B=1, Hq=16, L=16384: 36.1 against 19.2, the sequence cut into 64
+// chunks for one merging workgroup), more units (B=64, L=1024: 34.9 against
+// 33.0) and ragged lengths (B=64, lengths in [16, 4096]: 47.5 against 42.5).
 constexpr int64_t kHdMinBytes = 4000000;
 static bool hd_preferred(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                          int64_t total_tokens, int64_t max_tokens) {
-    if (head_dim != 64 && head_dim != 128) return false;
+    if ((head_dim != 64 && head_dim != 128) || num_kv_heads < 2) return false;
     const int64_t units = batch * num_kv_heads * query_blocks((int)(num_q_heads / num_kv_heads));
     const int64_t bytes = total_tokens * num_kv_heads * (head_dim + head_dim / 8);
-    return units <= 256 && bytes >= kHdMinBytes && bytes < kPagesMinBytes &&
+    return units <= 256 && (head_dim == 128 || bytes >= kHdMinBytes) && bytes < kPagesMinBytes &&
            4 * total_tokens >= 3 * batch * max_tokens;
 }
 

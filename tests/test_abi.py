@@ -257,7 +257,8 @@ def test_gqa8_plans():
     # lengths; the page-kernel bit keeps the page kernel's balanced mode; a
     # block table wider than 64 chunks of 64 tiles leaves the plan's choice to
     # the general kernel; a short batch goes to the head-dim kernel's
-    # token-page mode, a shorter one to the general kernel.
+    # token-page mode (at head_dim 64 only from 4 MB of K/V; never with one
+    # kv head).
     B, Hq, Hkv, D = 4, 64, 8, 128
     ct, mc, nw, ws = decode_plan(B, Hq, Hkv, D, 8192, B * 131072, 131072)
     assert (ct, mc, nw) == (64, 64, 16) and ws == pages_workspace(B, Hq, D, 64)
@@ -270,8 +271,11 @@ def test_gqa8_plans():
     assert decode_plan(1, Hq, Hkv, D, 8192, 131072, 131072)[2] <= 4   # one or two sequences: the general kernel
     assert decode_plan(2, Hq, Hkv, D, 8192, 2 * 131072, 131072)[2] <= 4
     assert decode_plan(3, Hq, Hkv, D, 4096, 3 * 65536, 65536)[2] == 16
-    assert decode_plan(B, Hq, Hkv, D, 64, B * 1024, 1024)[2] == 8 | 0x800  # 4.7 MB: the head-dim kernel
-    assert decode_plan(B, Hq, Hkv, D, 64, B * 512, 512)[2] <= 4             # 2.4 MB: the general kernel
+    assert decode_plan(B, Hq, Hkv, D, 64, B * 1024, 1024)[2] == 8 | 0x800  # the head-dim kernel
+    assert decode_plan(B, Hq, Hkv, D, 64, B * 512, 512)[2] == 8 | 0x800
+    assert decode_plan(B, 32, 8, 64, 64, B * 512, 512)[2] <= 4              # head_dim 64, 1.2 MB: general
+    assert decode_plan(B, 32, 8, 64, 256, B * 4096, 4096)[2] == 16 | 0x800  # head_dim 64, 9.4 MB
+    assert decode_plan(1, 16, 1, 128, 1024, 16384, 16384)[2] <= 4           # one kv head: general
 
 
 @pytest.mark.parametrize("cfg", [
@@ -347,8 +351,9 @@ def test_decode_plan_overrides_and_errors():
     assert int4_decode_plan(2, 8, 1, 96, 24, 10)[2] == 4 | 0x400
     assert int4_decode_plan(2, 8, 2, 256, 24, 10)[2] == 4 | 0x400
     assert int4_decode_plan(2, 8, 2, 128, 24, 10, waves_per_block=0x400)[2] == 4 | 0x400
-    assert int4_decode_plan(2, 8, 2, 128, 32, 10)[2] in (4, 16)
-    assert int4_decode_plan(2, 8, 2, 128, 48, 10)[2] in (1, 2, 3, 4, 16)
+    assert int4_decode_plan(2, 8, 2, 128, 32, 10)[2] in (4, 16, 8 | 0x800)
+    assert int4_decode_plan(2, 8, 2, 128, 48, 10)[2] in (1, 2, 3, 4, 16, 8 | 0x800)
+    assert int4_decode_plan(2, 8, 2, 128, 32, 10, waves_per_block=4)[2] == 4
     ct, mc, nw, ws = int4_decode_plan(3, 8, 2, 128, 8, 60, tokens_per_split=64)
     assert ct * 32 * mc >= 60 * 8 and ct % 8 == 0 and nw == 8 | 0x800
     ct, mc, nw, ws = int4_decode_plan(3, 8, 2, 128, 8, 60, tokens_per_split=64, waves_per_block=0x400)
