@@ -155,10 +155,12 @@ int iris_quantize_pack_int4(const void *x, void *packed, void *scales, int64_t n
 #define IRIS_DECODE_ANY_KERNEL 0x400
 /* IRIS_DECODE_TOKEN_PAGES: the MFMA kernel of head dims 96-224 in its
  * token-page mode, which takes every page size (each token's page looked
- * up through the table), at head_dim 64 to 224 in steps of 32 where
- * head_dim / 32 x num_kv_heads is even.  Asked for at other shapes,
- * iris_decode_plan returns the any-shape kernel's plan (out_waves then
- * carries IRIS_DECODE_ANY_KERNEL).  It is the bit to ask for when the page
+ * up through the table), at head_dim 64 to 224 in steps of 32 and any
+ * number of kv heads.  Asked for at other head dims, iris_decode_plan
+ * returns the any-shape kernel's plan (out_waves then carries
+ * IRIS_DECODE_ANY_KERNEL).  Where head_dim / 32 x num_kv_heads and
+ * num_pages x page_size are both odd (the scale tensors end on half a
+ * dword) the launch runs the any-shape kernel with the same plan.  It is the bit to ask for when the page
  * size is not a multiple of 16 up to 256; it may be asked for at any page
  * size.  The mode addresses token slots (page id x page_size + offset) in
  * 32 bits: a pool of at most 2^32 token slots. */
@@ -214,6 +216,8 @@ int iris_decode_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, i
  * up to 256 need a plan made with IRIS_DECODE_TOKEN_PAGES or
  * IRIS_DECODE_ANY_KERNEL.  max_pages is the number of
  * block_table columns; plan with ceil(max_pages * page_size / 16).
+ * num_pages is the pool's page count (k_data's first dimension): the
+ * token-page mode reads it to stay within the scale tensors.
  * Page ids and lengths are not
  * range-checked on the device (fused_attention.py:415-429 does that on the
  * host).  Tokens of the last page beyond seq_lens[b] are read but never

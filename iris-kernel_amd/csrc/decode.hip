@@ -1385,9 +1385,9 @@ constexpr int32_t kValuTile = IRIS_DECODE_VALU_TILE;
 constexpr int32_t kAnyKernel = IRIS_DECODE_ANY_KERNEL;
 constexpr int32_t kTokenPages = IRIS_DECODE_TOKEN_PAGES;
 // IRIS_DECODE_TOKEN_PAGES, a fourth bit: the head-dim kernel's token-page
-// mode (decode_hd.hip; every page size at head_dim 64-224 where
-// head_dim / 32 x num_kv_heads is even; the any-shape kernel's plan
-// elsewhere).  The caller of a page size that is not 16 m asks for it.
+// mode (decode_hd.hip; every page size at head_dim 64-224; the any-shape
+// kernel's plan elsewhere).  The caller of a page size that is not 16 m
+// asks for it.
 // The selection bits of waves_per_block, or -1 if it is not a valid request
 // (at most one bit).
 static int32_t selection_of(int32_t waves_per_block) {
@@ -1602,6 +1602,16 @@ extern "C" int iris_int4_paged_decode_attention(
         if (page_size < 1 || max_pages <= 0 || page_size > 0x3FFFFFFF || max_pages > 0x3FFFFFFF ||
             num_pages < 0 || num_pages > ((int64_t)1 << 32) || num_pages * page_size > ((int64_t)1 << 32))
             return kInvalidArgument;
+        // Odd scale rows (head_dim / 32 x Hkv odd) in a pool of an odd
+        // number of token slots: the scale tensors end on the first half of
+        // a dword, which the mode's dword loads of the last slot's last kv
+        // head would pass; such calls run on the any-shape kernel, which
+        // takes the same plan (chunks of 32-token tiles, an even count) and
+        // the same workspace layout.
+        if ((head_dim / 32 * num_kv_heads) % 2 != 0 && (num_pages * page_size) % 2 != 0)
+            return any_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
+                              workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim,
+                              page_size, max_pages, softmax_scale, chunk_tiles, max_chunks, stream);
         const int64_t pages16 = (max_pages * page_size + kPageSize - 1) / kPageSize;
         return hd_launch(query, k_data, v_data, k_scale, v_scale, block_table, seq_lens, output, output_is_f32,
                          workspace, workspace_bytes_avail, batch, num_q_heads, num_kv_heads, head_dim, pages16,

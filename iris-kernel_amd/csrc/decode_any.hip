@@ -37,6 +37,7 @@ namespace an {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTok = 64;       // tokens a tile, one a lane
+constexpr int kMergeBatch = 8;  // partials a merge round trip loads
 constexpr int kMaxHeads = 16;  // query heads a workgroup: a block of its kv head's
 constexpr int kHeadsPerWave = kMaxHeads / kWaves;
 constexpr int kMaxDim = 512;
@@ -309,22 +310,33 @@ __global__ __launch_bounds__(kThreads) void int4_decode_any_kernel(Args a) {
     if (*last == 0) return;
 
     // ---- merge the chunks in order: o = sum_c w_c (o / l)_c / sum_c w_c,
-    // w_c = l_c 2^(m_c - m*), m* the running maximum
+    // w_c = l_c 2^(m_c - m*), m* the running maximum; the partials of
+    // kMergeBatch chunks loaded together (one round trip a batch)
     for (int e = tid; e < nh * D; e += kThreads) {
         const int h = e / D, d = e - h * D, qh = hq0 + h;
         float mstar = -INFINITY, lsum = 0.0f, o = 0.0f;
-        for (int c = 0; c < n_chunks; ++c) {
-            const u32x2_t ml = __builtin_amdgcn_raw_buffer_load_b64(rm, (uint32_t)(((int64_t)c * hq + qh) * 8), 0, kSC1);
-            const float oc = __builtin_bit_cast(
-                float, __builtin_amdgcn_raw_buffer_load_b32(ro, (uint32_t)((((int64_t)c * hq + qh) * D + d) * 4), 0, kSC1));
-            const float mc = as_f32(ml[0]), lc = as_f32(ml[1]);
-            const float mb = fmaxf(mstar, mc);
-            const bool none = mb == -INFINITY;
-            const float r = none ? 1.0f : __builtin_amdgcn_exp2f(mstar - mb);
-            const float w = none ? 0.0f : lc * __builtin_amdgcn_exp2f(mc - mb);
-            o = o * r + w * oc;
-            lsum = lsum * r + w;
-            mstar = mb;
+        for (int c0 = 0; c0 < n_chunks; c0 += kMergeBatch) {
+            u32x2_t ml[kMergeBatch];
+            float oc[kMergeBatch];
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) {
+                const int c = min(c0 + j, n_chunks - 1);
+                ml[j] = __builtin_amdgcn_raw_buffer_load_b64(rm, (uint32_t)(((int64_t)c * hq + qh) * 8), 0, kSC1);
+                oc[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                      ro, (uint32_t)((((int64_t)c * hq + qh) * D + d) * 4), 0, kSC1));
+            }
+#pragma unroll
+            for (int j = 0; j < kMergeBatch; ++j) {
+                if (c0 + j >= n_chunks) break;  // uniform
+                const float mc = as_f32(ml[j][0]), lc = as_f32(ml[j][1]);
+                const float mb = fmaxf(mstar, mc);
+                const bool none = mb == -INFINITY;
+                const float r = none ? 1.0f : __builtin_amdgcn_exp2f(mstar - mb);
+                const float w = none ? 0.0f : lc * __builtin_amdgcn_exp2f(mc - mb);
+                o = o * r + w * oc[j];
+                lsum = lsum * r + w;
+                mstar = mb;
+            }
         }
         const float res = o / lsum;
         const int64_t at = ((int64_t)b * hq + qh) * D + d;
@@ -375,9 +387,16 @@ int any_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t h
         chunk_tok = round_up(tokens_per_split, an::kTok);
     } else {
         // About 1024 workgroups (four a CU): as many chunks of the longest
-        // sequence as that leaves room for.
+        // sequence as that leaves room for; but no more than 64 partial
+        // elements a thread for the merging workgroup (one round trip per
+        // kMergeBatch chunks; MI355X, B=1, Hq=16, Hkv=1, D=96, L=16384: 256
+        // chunks took 411 us).
         int64_t per = (1024 + units - 1) / units;
         if (per < 1) per = 1;
+        const int64_t nh = g < an::kMaxHeads ? g : an::kMaxHeads;
+        const int64_t per_thread = (nh * head_dim + an::kThreads - 1) / an::kThreads;
+        const int64_t most = 64 / per_thread > 1 ? 64 / per_thread : 1;
+        if (per > most) per = most;
         chunk_tok = round_up((max_tokens + per - 1) / per, an::kTok);
     }
     // The arrival counters of a sequence: one per (kv head, query block).

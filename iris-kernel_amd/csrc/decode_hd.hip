@@ -7,8 +7,8 @@
 // for head_dim 96, 160, 192 and 224 (G = 3, 5, 6, 7 scale groups of 32
 // dims), any number of kv heads and of query heads per kv head, pages of
 // 16 m tokens; in token-page mode (TOK) for head_dim 64 to 224 (G = 2-7)
-// where G x Hkv is even and pages of any size, each token's page looked up
-// through the block table.  It computes the result of
+// and pages of any size, each token's page looked up through the block
+// table (ODD: the scale shifts per token, where G x Hkv is odd).  It computes the result of
 // `torch_eager_int4_paged_decode_attention`
 // (src/iris_kernel/torch_eager_attention.py:154-239), which takes any head
 // dim that is a multiple of the group size (:93) and any page size (:72)
@@ -367,9 +367,12 @@ __device__ __forceinline__ void aligned_scales(const u32x4_t (&raw)[2][Geo<G>::S
 }
 
 // TOK: token-page mode (any page size; a tile's tokens looked up one by one
-// through the block table); otherwise pages of 16 m tokens.
-template <int G, bool TOK>
+// through the block table); otherwise pages of 16 m tokens.  ODD (token
+// pages only): Hkv x G odd, so a kv head's scales start on either half of a
+// dword depending on the token's slot; the shift is then taken per token.
+template <int G, bool TOK, bool ODD>
 __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) {
+    static_assert(TOK || !ODD, "per-token scale shifts are a token-page mode");
     using L = Geo<G>;
     constexpr int D = L::D, HB = L::HB, W = L::W, NK = L::NK, NS = L::NS, SP = L::SP, SLOT = L::SLOT;
     extern __shared__ __align__(16) uint8_t smem[];
@@ -511,8 +514,11 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     // one tile before the tile's data loads; then each lane turns its entry
     // into the token's slot in the pool (entry * page_size + token %
     // page_size) and every load lane takes its token's slot with
-    // ds_bpermute.  The scale shift of a token is uniform because the mode
-    // is taken only where Hkv * G is even.
+    // ds_bpermute.  With Hkv * G even every token's kv head starts on the
+    // same half of a scale dword ((kvh G) & 1); with it odd (ODD) the half is
+    // the parity of slot Hkv G + kvh G, taken per token: for the loads, and,
+    // as a 32-bit mask of the tile's tokens (a ballot at the slot lookup),
+    // for the reads.
     uint8_t* const ent_base = smem + L::ID_OFF + wave * L::ID_BYTES;
     const int psz = a.page_size;
     auto issue_entries = [&](int s) __attribute__((always_inline)) {
@@ -521,14 +527,17 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(bt + min(tg / psz, a.bt_cols - 1)),
                                              (IRIS_LDS void*)(ent_base + (s & 1) * 128), 4, 0, 0);
     };
-    auto slots_of = [&](int s) __attribute__((always_inline)) -> uint32_t {
-        const uint32_t e = lds_read_b32(lds_addr(ent_base + (s & 1) * 128) + 4 * (lane & 31));
-        const int tg = min((t_begin + W * s + wave) * kTile + (lane & 31), seq_len - 1);
-        return e * (uint32_t)psz + (uint32_t)(tg % psz);  // a pool of at most 2^32 token slots
-    };
     const int64_t row_bytes = (int64_t)a.n_kv_heads * HB;       // a token row of a code tensor
     const int64_t srow_halves = (int64_t)a.n_kv_heads * G;      // a token row of a scale tensor
     const int tok_sh = (kvh * G) & 1;                           // (Hkv * G even)
+    auto slots_of = [&](int s, uint32_t& odd_mask) __attribute__((always_inline)) -> uint32_t {
+        const uint32_t e = lds_read_b32(lds_addr(ent_base + (s & 1) * 128) + 4 * (lane & 31));
+        const int tg = min((t_begin + W * s + wave) * kTile + (lane & 31), seq_len - 1);
+        const uint32_t slot = e * (uint32_t)psz + (uint32_t)(tg % psz);  // a pool of at most 2^32 token slots
+        if constexpr (ODD)  // bit t: token t's kv head starts on the second half of a dword
+            odd_mask = (uint32_t)__ballot(((slot * (uint32_t)srow_halves + (uint32_t)(kvh * G)) & 1u) != 0);
+        return slot;
+    };
     auto issue_tok = [&](int slot, uint32_t slots) __attribute__((always_inline)) {
         uint8_t* const dst = ring + slot * SLOT;
 #pragma unroll
@@ -549,8 +558,14 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
             const int p = 64 * i + lane;
             const int t = p / SP, j = p % SP;
             const uint32_t st = __builtin_amdgcn_ds_bpermute(4 * t, (int)slots);
-            if (sc_ok[i]) {
-                const int64_t off = (((int64_t)st * srow_halves + kvh * G) - tok_sh) * 2 + 4 * j;
+            int sh = tok_sh;
+            bool ok = sc_ok[i];
+            if constexpr (ODD) {
+                sh = (int)((st * (uint32_t)srow_halves + (uint32_t)(kvh * G)) & 1u);
+                ok = 2 * j < G + sh;  // (j = 0 in every token: each load has a lane)
+            }
+            if (ok) {
+                const int64_t off = (((int64_t)st * srow_halves + kvh * G) - sh) * 2 + 4 * j;
                 __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.k_scale + off),
                                                  (IRIS_LDS void*)(dst + L::KS_OFF + 256 * i), 4, 0, 0);
                 __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.v_scale + off),
@@ -614,7 +629,13 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
 
     // One tile whose slot has landed: s[e][i] is token 16 e + 4 jq + i,
     // query head n.
-    auto compute = [&](int tile, uint32_t base) __attribute__((always_inline)) {
+    // odd_mask: the tile's per-token scale shifts (ODD; see slots_of)
+    auto compute = [&](int tile, uint32_t base, uint32_t odd_mask) __attribute__((always_inline)) {
+        // the half shift of the scales of token 16 e + 4 jq + i
+        auto shift_of = [&](int e, int i) -> uint32_t {
+            if constexpr (ODD) return ((odd_mask >> (16 * e + 4 * jq + i)) & 1u) * 16u;
+            else return shift[i];
+        };
         const int tok0 = tile * kTile;
         const bool full = tok0 + kTile <= seq_len;
         uint32_t kw[2][G];
@@ -630,7 +651,7 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 uint32_t ks[L::NA];
-                aligned_scales<G>(sraw, e, i, shift[i], ks);
+                aligned_scales<G>(sraw, e, i, shift_of(e, i), ks);
                 float sc = 0.0f;
 #pragma unroll
                 for (int g = 0; g < G; ++g) sc = __builtin_fmaf((float)as_half2(ks[g >> 1])[g & 1], acc[g][i], sc);
@@ -688,7 +709,7 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
 #pragma unroll
         for (int e = 0; e < 2; ++e)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) aligned_scales<G>(sraw, e, i, shift[i], vs[e][i]);
+            for (int i = 0; i < 4; ++i) aligned_scales<G>(sraw, e, i, shift_of(e, i), vs[e][i]);
         if (!full) {
             // Tokens past seq_len may hold any bytes: never let their scale
             // reach the product (0 * NaN).  A real branch.
@@ -734,12 +755,13 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     constexpr int JOBS = 2 * NK + 2 * NS;
     static_assert(JOBS + 2 < 64, "vmcnt range");
     const uint32_t ring_addr = lds_addr(ring);
+    uint32_t odd_cur = 0, odd_next = 0;  // (ODD) the scale shifts of tiles s and s + 1
     if constexpr (TOK) {
         // entries of tiles 0 and 1, then the data of tile 0
         if (n_my > 0) issue_entries(0);
         if (n_my > 1) issue_entries(1);
         wait_vmcnt<0>();
-        if (n_my > 0) issue_tok(0, slots_of(0));
+        if (n_my > 0) issue_tok(0, slots_of(0, odd_cur));
     } else {
         if (n_my > 0) issue(0, 0);
     }
@@ -751,7 +773,7 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
                 wait_vmcnt<JOBS>();  // tile s
             } else {
                 wait_vmcnt<JOBS>();  // the entries of tile s + 1 (tile s's data may fly)
-                const uint32_t sl = slots_of(s + 1);
+                const uint32_t sl = slots_of(s + 1, odd_next);
                 if (s + 2 < n_my) {
                     issue_entries(s + 2);
                     issue_tok(next, sl);
@@ -764,7 +786,8 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
         } else {
             wait_vmcnt<0>();
         }
-        compute(t_begin + W * s + wave, ring_addr + (uint32_t)((s & 1) * SLOT));
+        compute(t_begin + W * s + wave, ring_addr + (uint32_t)((s & 1) * SLOT), odd_cur);
+        odd_cur = odd_next;
     }
     wait_vmcnt<0>();
     __syncthreads();
@@ -897,10 +920,7 @@ bool hd_supported(int64_t head_dim) {
 }
 
 bool hd_tok_supported(int64_t head_dim, int64_t num_kv_heads) {
-    // A token's scale row (Hkv G halves) is a whole number of dwords, so
-    // every token's kv head starts on the same half.
-    return head_dim % 32 == 0 && head_dim >= 64 && head_dim <= 224 && num_kv_heads > 0 &&
-           (head_dim / 32 * num_kv_heads) % 2 == 0;
+    return head_dim % 32 == 0 && head_dim >= 64 && head_dim <= 224 && num_kv_heads > 0;
 }
 
 int hd_waves(int64_t head_dim) {
@@ -958,6 +978,15 @@ int hd_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t he
         int64_t floor_tiles = (longest + per_unit - 1) / per_unit;
         if (floor_tiles > 8 * W) floor_tiles = 8 * W;
         chunk_tiles = share > floor_tiles ? share : floor_tiles;
+        // The merging workgroup reads every chunk's partial of its block of
+        // query heads, kMergeBatch chunks a round: at most 64 partial
+        // elements a thread (MI355X, B=1, Hq=16, Hkv=1, D=128, L=16384: 64
+        // chunks 36.3 us, 16 chunks 22.2).
+        const int64_t nh = num_q_heads / num_kv_heads < hd::kHeads ? num_q_heads / num_kv_heads : hd::kHeads;
+        const int64_t per_thread = (nh * head_dim + 64 * W - 1) / (64 * W);
+        const int64_t most = 64 / per_thread > 1 ? 64 / per_thread : 1;
+        const int64_t fewest_tiles = (longest + most - 1) / most;
+        if (chunk_tiles < fewest_tiles) chunk_tiles = fewest_tiles;
         if (chunk_tiles > longest) chunk_tiles = longest;
     }
     const int64_t cap = hd_max_chunk_tiles(W);
@@ -979,14 +1008,14 @@ int hd_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t he
 }
 
 namespace {
-template <int G, bool TOK>
+template <int G, bool TOK, bool ODD = false>
 int launch_hd(dim3 grid, hipStream_t s, const hd::Args& a) {
     using L = hd::Geo<G>;
     static std::atomic<uint64_t> lds_raised{0};
-    if (allow_full_lds(reinterpret_cast<const void*>(&hd::int4_decode_hd_kernel<G, TOK>), lds_raised) != kOk)
+    if (allow_full_lds(reinterpret_cast<const void*>(&hd::int4_decode_hd_kernel<G, TOK, ODD>), lds_raised) != kOk)
         return kLaunchError;
-    hipLaunchKernelGGL((hd::int4_decode_hd_kernel<G, TOK>), grid, dim3(64 * L::W), TOK ? L::LDS_BYTES_TOK : L::LDS_BYTES,
-                       s, a);
+    hipLaunchKernelGGL((hd::int4_decode_hd_kernel<G, TOK, ODD>), grid, dim3(64 * L::W),
+                       TOK ? L::LDS_BYTES_TOK : L::LDS_BYTES, s, a);
     return hipGetLastError() == hipSuccess ? kOk : kLaunchError;
 }
 }  // namespace
@@ -1053,13 +1082,15 @@ int hd_launch(const void* query, const void* k_data, const void* v_data, const v
     const dim3 grid((unsigned)nblocks);
     hipStream_t s = (hipStream_t)stream;
     if (token_pages) {
+        // Hkv x G odd: the scale shifts per token (G odd and Hkv odd)
+        const bool odd = (head_dim / 32 * num_kv_heads) % 2 != 0;
         switch (head_dim) {
             case 64: return launch_hd<2, true>(grid, s, a);
-            case 96: return launch_hd<3, true>(grid, s, a);
+            case 96: return odd ? launch_hd<3, true, true>(grid, s, a) : launch_hd<3, true>(grid, s, a);
             case 128: return launch_hd<4, true>(grid, s, a);
-            case 160: return launch_hd<5, true>(grid, s, a);
+            case 160: return odd ? launch_hd<5, true, true>(grid, s, a) : launch_hd<5, true>(grid, s, a);
             case 192: return launch_hd<6, true>(grid, s, a);
-            default: return launch_hd<7, true>(grid, s, a);
+            default: return odd ? launch_hd<7, true, true>(grid, s, a) : launch_hd<7, true>(grid, s, a);
         }
     }
     switch (head_dim) {

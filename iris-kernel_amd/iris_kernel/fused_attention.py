@@ -53,8 +53,8 @@ DECODE_VALU_TILE = 0x200
 DECODE_ANY_KERNEL = 0x400
 # The token-page mode of the head-dim MFMA kernel (IRIS_DECODE_TOKEN_PAGES):
 # every page size, each token's page looked up through the block table, at
-# head_dim 64 to 224 (steps of 32) where head_dim / 32 * num_kv_heads is
-# even; asked for at other shapes, the plan returns the any-shape kernel's.
+# head_dim 64 to 224 (steps of 32); asked for at other head dims, the plan
+# returns the any-shape kernel's.
 DECODE_TOKEN_PAGES = 0x800
 
 

@@ -92,13 +92,15 @@ def test_decode_rejects_unsupported_shapes_before_launch():
     assert call(P=48, nw=any_, ct=2, mc=3) == 3             # three chunks need a workspace
     assert call(nw=0x400 | 0x100) == 1                      # one selection bit at most
     assert call(nw=0x800 | 0x400) == 1
-    # the token-page mode: any page size, head_dim 64-224 with D / 32 x Hkv even
+    # the token-page mode: any page size, head_dim 64-224
     tok = 0x800
     assert call(D=96, P=24, nw=12 | tok, ct=12, mc=1) == 2   # valid: it gets as far as the launch
     assert call(D=64, P=1, nw=16 | tok, ct=16, mc=1) == 2
     assert call(D=128, P=8, nw=8 | tok, ct=8, mc=1) == 2
     assert call(D=224, P=16, nw=8 | tok, ct=8, mc=1) == 2   # 16-token pages too
-    assert call(D=96, P=24, Hkv=1, nw=12 | tok, ct=12, mc=1) == 1  # 3 x 1 scale halves a row: odd
+    assert call(D=96, P=24, Hkv=1, nw=12 | tok, ct=12, mc=1) == 2  # 3 x 1 scale halves a row: odd
+    assert call(D=96, P=3, NP=7, Hkv=1, nw=12 | tok, ct=12, mc=1) == 2  # ... in an odd pool: the any kernel
+    assert call(D=96, P=3, NP=7, Hkv=1, nw=12 | tok, ct=3, mc=1) == 1   # (whose chunks are even tile counts)
     assert call(D=256, P=8, nw=8 | tok, ct=8, mc=1) == 1    # head_dim 64 to 224
     assert call(D=96, P=24, nw=8 | tok, ct=12, mc=1) == 1   # its wave count only
     assert call(D=96, P=0, nw=12 | tok, ct=12, mc=1) == 1   # page_size >= 1
@@ -333,7 +335,7 @@ def test_decode_plan_overrides_and_errors():
     assert decode_plan(2, 8, 2, 64, 64, waves_per_block=0x800)[2] == 16 | 0x800
     assert decode_plan(2, 8, 1, 64, 64, waves_per_block=0x800)[2] == 16 | 0x800
     assert decode_plan(2, 8, 2, 96, 64, waves_per_block=0x800)[2] == 12 | 0x800
-    assert decode_plan(2, 8, 1, 96, 64, waves_per_block=0x800)[2] == 4 | 0x400   # 3 halves a row
+    assert decode_plan(2, 8, 1, 96, 64, waves_per_block=0x800)[2] == 12 | 0x800  # 3 halves a row
     assert decode_plan(2, 8, 2, 256, 64, waves_per_block=0x800)[2] == 4 | 0x400
     assert decode_plan(2, 8, 2, 288, 64, waves_per_block=0x800)[2] == 4 | 0x400
     ct, mc, nw, ws = decode_plan(2, 8, 2, 160, 64, tokens_per_split=256, waves_per_block=0x800)
@@ -348,7 +350,8 @@ def test_decode_plan_overrides_and_errors():
     assert int4_decode_plan(2, 8, 2, 128, 24, 10)[2] == 8 | 0x800
     assert int4_decode_plan(2, 8, 2, 128, 1, 1000)[2] == 8 | 0x800
     assert int4_decode_plan(2, 8, 2, 128, 272, 10)[2] == 8 | 0x800
-    assert int4_decode_plan(2, 8, 1, 96, 24, 10)[2] == 4 | 0x400
+    assert int4_decode_plan(2, 8, 1, 96, 24, 10)[2] == 12 | 0x800
+    assert int4_decode_plan(2, 8, 1, 256, 24, 10)[2] == 4 | 0x400
     assert int4_decode_plan(2, 8, 2, 256, 24, 10)[2] == 4 | 0x400
     assert int4_decode_plan(2, 8, 2, 128, 24, 10, waves_per_block=0x400)[2] == 4 | 0x400
     assert int4_decode_plan(2, 8, 2, 128, 32, 10)[2] in (4, 16, 8 | 0x800)

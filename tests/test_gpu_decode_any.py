@@ -136,30 +136,30 @@ def test_any_kernel_forced_at_fast_shapes(device, cfg):
 
 def test_positional_handle_at_any_shape(device):
     # The sync-free positional handle plans for the widest batch the block
-    # table admits, at a 24-token page and head_dim 96 on one kv head (3
-    # scale halves a token row: the token-page mode does not take it).
-    q, cache, bt, sl = _case(8, 1, 96, 24, [40, 900], 5)
-    assert int4_decode_plan(2, 8, 1, 96, 24, bt.shape[1])[2] & DECODE_ANY_KERNEL
+    # table admits, at a 24-token page and head_dim 256 (the token-page mode
+    # takes head dims up to 224).
+    q, cache, bt, sl = _case(8, 2, 256, 24, [40, 900], 5)
+    assert int4_decode_plan(2, 8, 2, 256, 24, bt.shape[1])[2] & DECODE_ANY_KERNEL
     want = torch_eager_int4_paged_decode_attention(q, *cache, bt, sl, page_size=24, out_dtype=torch.float32)
     gq, gbt, gsl = to(device, q, bt, sl)
     out = torch.empty(q.shape, dtype=torch.float32, device=device)
-    _int4_paged_decode_attention(gq, *to(device, *cache), gbt, gsl, out, 96, 24)
+    _int4_paged_decode_attention(gq, *to(device, *cache), gbt, gsl, out, 256, 24)
     torch.cuda.synchronize(device)
-    assert_attention_close(out, want, "positional handle D=96 P=24")
+    assert_attention_close(out, want, "positional handle D=256 P=24")
 
 
 def test_hip_graph_replay_at_any_shape(device):
-    # The sync-free positional handle at head_dim 160 on one kv head and
+    # The sync-free positional handle at head_dim 320 on one kv head and
     # 8-token pages (split-KV: it plans for the widest batch the table
     # admits), captured in a HIP graph: every replay, with eager work in
     # between, equals the eager launch bit for bit.
-    q, cache, bt, sl = _case(16, 1, 160, 8, [500, 1500, 64], 9)
+    q, cache, bt, sl = _case(16, 1, 320, 8, [500, 1500, 64], 9)
     gq, gbt, gsl = to(device, q, bt, sl)
     gcache = to(device, *cache)
-    plan = int4_decode_plan(3, 16, 1, 160, 8, bt.shape[1])
+    plan = int4_decode_plan(3, 16, 1, 320, 8, bt.shape[1])
     assert plan[1] > 1 and plan[2] & DECODE_ANY_KERNEL, plan
     eager = torch.empty(q.shape, dtype=torch.float32, device=device)
-    _int4_paged_decode_attention(gq, *gcache, gbt, gsl, eager, 160, 8)
+    _int4_paged_decode_attention(gq, *gcache, gbt, gsl, eager, 320, 8)
     torch.cuda.synchronize(device)
     want = torch_eager_int4_paged_decode_attention(q, *cache, bt, sl, page_size=8, out_dtype=torch.float32)
     assert_attention_close(eager, want, "graph case eager")
@@ -167,11 +167,11 @@ def test_hip_graph_replay_at_any_shape(device):
     s = torch.cuda.Stream(device)
     s.wait_stream(torch.cuda.current_stream(device))
     with torch.cuda.stream(s):
-        _int4_paged_decode_attention(gq, *gcache, gbt, gsl, out, 160, 8)  # warm-up on the side stream
+        _int4_paged_decode_attention(gq, *gcache, gbt, gsl, out, 320, 8)  # warm-up on the side stream
     torch.cuda.current_stream(device).wait_stream(s)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        _int4_paged_decode_attention(gq, *gcache, gbt, gsl, out, 160, 8)
+        _int4_paged_decode_attention(gq, *gcache, gbt, gsl, out, 320, 8)
     for i in range(4):
         out.fill_(float("nan"))
         torch.randn(1000, device=device).sum()  # eager work between replays

@@ -3,9 +3,9 @@ head-dim MFMA kernel (csrc/decode_hd.hip, IRIS_DECODE_TOKEN_PAGES): each of
 a tile's 32 tokens finds its page through the block table, so the page size
 is free (the reference's eager path takes any page size,
 torch_eager_attention.py:72; its fused path only 16, fused_attention.py:
-390-403).  Head dims 64 to 224 in steps of 32 where head_dim / 32 x
-num_kv_heads is even (a token's scale row is whole dwords); other shapes
-plan the any-shape kernel.  Checked against the checker's eager attention
+390-403).  Head dims 64 to 224 in steps of 32, any number of kv heads (where
+head_dim / 32 x num_kv_heads is odd, a kv head's scales start on either
+half of a dword, by the token's slot, and the shift is taken per token).  Checked against the checker's eager attention
 (fp32 values within helpers.ATOL; fp16 outputs within one ulp), with one
 chunk a sequence and with split-KV, against the any-shape kernel, on caches
 written by the package's own append, through the positional handle and in
@@ -99,15 +99,32 @@ def test_token_pages_agree_with_the_any_kernel(device, d, page):
     log(f"decode tok: D={d} P={page} against the any kernel {e:.2e}")
 
 
-def test_odd_scale_rows_fall_back_to_the_any_kernel(device):
-    # head_dim 96 on one or three kv heads: 3 or 9 scale halves a token row,
-    # so kv heads start on either half of a dword; the plan takes the
-    # any-shape kernel, whose result is checked as well.
-    for hq, hkv in ((8, 1), (9, 3)):
-        q, cache, bt, sl = _case(hq, hkv, 96, 24, [300, 1000], hkv)
-        plan = int4_decode_plan(2, hq, hkv, 96, 24, bt.shape[1], int(sl.sum()), int(sl.max()))
-        assert plan[2] & DECODE_ANY_KERNEL and not plan[2] & DECODE_TOKEN_PAGES, plan
-        _check(device, q, cache, bt, sl, 24, f"Hkv={hkv} D=96 P=24 (any)")
+@pytest.mark.parametrize("tps", [0, 128])
+@pytest.mark.parametrize("hq,hkv,d,page,lens", [
+    (8, 1, 96, 24, [300, 1000]),                  # 3 scale halves a token row
+    (9, 3, 96, 8, [1, 33, 700]),                  # 9
+    (5, 5, 160, 12, [100, 1500]),                 # 25
+    (7, 1, 224, 40, [41, 2000]),                  # 7
+    (16, 1, 96, 1, [1, 2, 31, 500]),              # one token a page
+    (3, 3, 160, 16, [16, 47, 900]),               # 16-token pages, asked for
+])
+def test_odd_scale_rows(device, hq, hkv, d, page, lens, tps):
+    # head_dim / 32 x Hkv odd: a kv head's scales start on either half of a
+    # dword, by the token's slot; the mode takes the shift per token.  In a
+    # pool of an even number of token slots the token-page mode runs; in an
+    # odd one (the scale tensors end on half a dword) the launch takes the
+    # any-shape kernel with the same plan.
+    kw = {"waves_per_block": DECODE_TOKEN_PAGES} if page % 16 == 0 else {}
+    for spare in (2, 3):
+        q, cache, bt, sl = _case(hq, hkv, d, page, lens, hq + d + page + spare + tps, spare=spare)
+        slots = cache[0].shape[0] * page
+        plan = int4_decode_plan(len(lens), hq, hkv, d, page, bt.shape[1], int(sl.sum()), int(sl.max()), tps,
+                                kw.get("waves_per_block", 0))
+        assert plan[2] == _waves(d) | DECODE_TOKEN_PAGES, plan
+        what = f"odd rows Hq={hq} Hkv={hkv} D={d} P={page} slots={slots} split={tps}"
+        log(f"decode tok: {what}")
+        _, e32, e16 = _check(device, q, cache, bt, sl, page, what, tokens_per_split=tps, **kw)
+        log(f"decode tok: {what}: fp32 {e32:.2e} fp16 {e16:.2e}")
 
 
 @pytest.mark.parametrize("d,page,hkv", [(128, 8, 2), (96, 24, 4), (224, 40, 2), (64, 1, 1)])

@@ -59,6 +59,7 @@ KERNELS = [
     ("d96-any", 8, 2, 96, DECODE_ANY_KERNEL),
     ("gqa-tok", 32, 8, 128, DECODE_TOKEN_PAGES),
     ("d96-tok", 8, 2, 96, DECODE_TOKEN_PAGES),
+    ("d96-tok-odd", 8, 1, 96, DECODE_TOKEN_PAGES),
 ]
 
 # (name, what is poisoned): sequence b, token t < L_b, kv head, scale group.

@@ -1,6 +1,7 @@
 """The head_dim 96-224 decode kernel's tile loop, checked in its compiled
 gfx950 code (csrc/decode_hd.hip, every G instance of both modes: pages of
-16 m tokens, and token pages at head_dim 64-224).
+16 m tokens, and token pages at head_dim 64-224, with the per-token scale
+shifts of odd scale rows at G = 3, 5, 7).
 
 A wave keeps the next tile's direct-to-LDS loads in flight while it
 computes one, which holds only if every vmcnt wait in the loop is one of the
@@ -22,7 +23,9 @@ from iris_kernel import _build
 
 SRC = _build.CSRC / "decode_hd.hip"
 GROUPS = [3, 5, 6, 7]  # head_dim / 32
-INSTANCES = [(g, False) for g in GROUPS] + [(g, True) for g in (2, 3, 4, 5, 6, 7)]
+# (G, token pages, per-token scale shifts)
+INSTANCES = ([(g, False, False) for g in GROUPS] + [(g, True, False) for g in (2, 3, 4, 5, 6, 7)]
+             + [(g, True, True) for g in (3, 5, 7)])
 
 
 def jobs_of(g: int) -> int:
@@ -48,8 +51,8 @@ def asm(tmp_path_factory):
     return out.read_text()
 
 
-def kernel(asm: str, g: int, tok: bool) -> list[str]:
-    sym = f"_ZN4iris2hd21int4_decode_hd_kernelILi{g}ELb{int(tok)}EEEvNS0_4ArgsE"
+def kernel(asm: str, g: int, tok: bool, odd: bool) -> list[str]:
+    sym = f"_ZN4iris2hd21int4_decode_hd_kernelILi{g}ELb{int(tok)}ELb{int(odd)}EEEvNS0_4ArgsE"
     body = asm[asm.index(sym + ":"):]
     body = body[:body.index(".Lfunc_end")]
     return [l.strip() for l in body.split("\n")]
@@ -69,17 +72,17 @@ def tile_loop(lines: list[str]) -> list[str]:
     return out
 
 
-@pytest.mark.parametrize("g,tok", INSTANCES)
-def test_tile_loop_is_the_tile_loop(asm, g, tok):
-    loop = tile_loop(kernel(asm, g, tok))
+@pytest.mark.parametrize("g,tok,odd", INSTANCES)
+def test_tile_loop_is_the_tile_loop(asm, g, tok, odd):
+    loop = tile_loop(kernel(asm, g, tok, odd))
     # per tile: 2 G QK and 2 G PV products, G transposed V reads
     assert sum(1 for l in loop if l.startswith("v_mfma")) == 4 * g
     assert sum(1 for l in loop if l.startswith("ds_read_b64_tr_b8")) == g
 
 
-@pytest.mark.parametrize("g,tok", INSTANCES)
-def test_tile_loop_waits_only_for_its_own_tiles(asm, g, tok):
-    loop = tile_loop(kernel(asm, g, tok))
+@pytest.mark.parametrize("g,tok,odd", INSTANCES)
+def test_tile_loop_waits_only_for_its_own_tiles(asm, g, tok, odd):
+    loop = tile_loop(kernel(asm, g, tok, odd))
     jobs = jobs_of(g)
     loads = sum(1 for l in loop if l.startswith("global_load_lds"))
     waits = {int(m) for l in loop if l.startswith("s_waitcnt") for m in re.findall(r"vmcnt\((\d+)\)", l)}
@@ -96,9 +99,9 @@ def test_tile_loop_waits_only_for_its_own_tiles(asm, g, tok):
         assert waits <= {0, jobs, jobs + 1}, (jobs, sorted(waits))
 
 
-@pytest.mark.parametrize("g,tok", INSTANCES)
-def test_tile_loop_is_uniform_and_nothing_spills(asm, g, tok):
-    lines = kernel(asm, g, tok)
+@pytest.mark.parametrize("g,tok,odd", INSTANCES)
+def test_tile_loop_is_uniform_and_nothing_spills(asm, g, tok, odd):
+    lines = kernel(asm, g, tok, odd)
     loop = tile_loop(lines)
     assert not [l for l in loop if re.match(r"s_andn2_b64\s+exec, exec", l)]  # no divergent-loop exit
     assert not [l for l in loop if l.startswith("v_readfirstlane")]
