@@ -387,16 +387,18 @@ int any_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t h
         chunk_tok = round_up(tokens_per_split, an::kTok);
     } else {
         // About 1024 workgroups (four a CU): as many chunks of the longest
-        // sequence as that leaves room for; but no more than 64 partial
-        // elements a thread for the merging workgroup (one round trip per
-        // kMergeBatch chunks; MI355X, B=1, Hq=16, Hkv=1, D=96, L=16384: 256
-        // chunks took 411 us).
+        // sequence as that leaves room for; with fewer than 16 units, no
+        // more than 64 partial elements a thread for the merging workgroup
+        // (one round trip per kMergeBatch chunks; MI355X, B=1, Hq=16, Hkv=1,
+        // D=96, L=16384: 256 chunks 411 us, 10 chunks 279; with more units
+        // the workgroups' count matters more: B=4, Hq=64, Hkv=8, D=160,
+        // L=32768: 32 chunks 469 us, 12 chunks 599).
         int64_t per = (1024 + units - 1) / units;
         if (per < 1) per = 1;
         const int64_t nh = g < an::kMaxHeads ? g : an::kMaxHeads;
         const int64_t per_thread = (nh * head_dim + an::kThreads - 1) / an::kThreads;
         const int64_t most = 64 / per_thread > 1 ? 64 / per_thread : 1;
-        if (per > most) per = most;
+        if (units < 16 && per > most) per = most;
         chunk_tok = round_up((max_tokens + per - 1) / per, an::kTok);
     }
     // The arrival counters of a sequence: one per (kv head, query block).
