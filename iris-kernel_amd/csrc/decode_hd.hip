@@ -75,7 +75,9 @@ struct Geo {
     static constexpr int R = 2;
     static constexpr int NK = (32 * G_ + 63) / 64;  // 16-byte loads a tensor a tile
     static constexpr int KA = 512 * G_;             // code area of a slot, per tensor (32 G pieces)
-    static constexpr int SD = G_ / 2 + 1;                    // scale dwords a token needs (at most)
+    // scale dwords a token needs (at most): G halves from its first one, which
+    // is the second half of a dword only where G is odd
+    static constexpr int SD = (G_ + (G_ & 1)) / 2;
     static constexpr int SP = SD <= 2 ? 2 : 4;               // scale dwords a token occupies in LDS
     static constexpr int NS = 32 * SP / 64;                  // 4-byte loads a scale tensor a tile
     static constexpr int NA = (G_ + 1) / 2;                  // aligned scale dwords a token
@@ -238,19 +240,18 @@ struct Reads<2> {
 template <>
 struct Reads<4> {
     static __device__ __forceinline__ void k(uint32_t kb0, uint32_t kb1, uint32_t sb, uint32_t (&k)[2][4],
-                                             u32x4_t (&s)[2][4]) {
+                                             u32x4_t (&s)[2][2]) {
         asm volatile(IRIS_R32(0, kb0, 0) IRIS_R32(1, kb0, 16) IRIS_R32(2, kb0, 32) IRIS_R32(3, kb0, 48)
                          IRIS_R32(4, kb1, 0) IRIS_R32(5, kb1, 16) IRIS_R32(6, kb1, 32) IRIS_R32(7, kb1, 48)
-                             IRIS_S4(8, 9, 10, 11, 12, 13, 14, 15) IRIS_WAIT
+                             IRIS_S2(8, 9, 10, 11) IRIS_WAIT
                      : "=&v"(k[0][0]), "=&v"(k[0][1]), "=&v"(k[0][2]), "=&v"(k[0][3]), "=&v"(k[1][0]),
-                       "=&v"(k[1][1]), "=&v"(k[1][2]), "=&v"(k[1][3]), IRIS_S4_OUT(s)
+                       "=&v"(k[1][1]), "=&v"(k[1][2]), "=&v"(k[1][3]), IRIS_S2_OUT(s)
                      : [kb0] "v"(kb0), [kb1] "v"(kb1), [sb] "v"(sb)
                      : "memory");
     }
-    static __device__ __forceinline__ void v(uint32_t tb, uint32_t sb, int2v_t (&v)[4], u32x4_t (&s)[2][4]) {
-        asm volatile(IRIS_TR(0, 0) IRIS_TR(1, 16) IRIS_TR(2, 32) IRIS_TR(3, 48) IRIS_S4(4, 5, 6, 7, 8, 9, 10, 11)
-                         IRIS_WAIT
-                     : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), IRIS_S4_OUT(s)
+    static __device__ __forceinline__ void v(uint32_t tb, uint32_t sb, int2v_t (&v)[4], u32x4_t (&s)[2][2]) {
+        asm volatile(IRIS_TR(0, 0) IRIS_TR(1, 16) IRIS_TR(2, 32) IRIS_TR(3, 48) IRIS_S2(4, 5, 6, 7) IRIS_WAIT
+                     : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), IRIS_S2_OUT(s)
                      : [tb] "v"(tb), [sb] "v"(sb)
                      : "memory");
     }

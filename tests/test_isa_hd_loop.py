@@ -30,8 +30,9 @@ INSTANCES = ([(g, False, False) for g in GROUPS] + [(g, True, False) for g in (2
 
 def jobs_of(g: int) -> int:
     """Load instructions of one tile: 16-byte code loads (32 g pieces of 64
-    lanes) and 4-byte scale loads (2 or 4 dwords a token), for K and V."""
-    sp = 2 if g // 2 + 1 <= 2 else 4
+    lanes) and 4-byte scale loads (2 or 4 dwords a token: g halves from the
+    first, on the second half of a dword only where g is odd), for K and V."""
+    sp = 2 if (g + (g & 1)) // 2 <= 2 else 4
     return 2 * ((32 * g + 63) // 64) + 2 * (32 * sp // 64)
 
 
