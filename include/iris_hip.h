@@ -155,7 +155,7 @@ int iris_quantize_pack_int4(const void *x, void *packed, void *scales, int64_t n
 #define IRIS_DECODE_ANY_KERNEL 0x400
 /* IRIS_DECODE_TOKEN_PAGES: the MFMA kernel of head dims 96-224 in its
  * token-page mode, which takes every page size (each token's page looked
- * up through the table), at head_dim 64 to 224 in steps of 32 and any
+ * up through the table), at head_dim 64 to 256 in steps of 32 and any
  * number of kv heads.  Asked for at other head dims, iris_decode_plan
  * returns the any-shape kernel's plan (out_waves then carries
  * IRIS_DECODE_ANY_KERNEL).  Where head_dim / 32 x num_kv_heads and

@@ -1385,7 +1385,7 @@ constexpr int32_t kValuTile = IRIS_DECODE_VALU_TILE;
 constexpr int32_t kAnyKernel = IRIS_DECODE_ANY_KERNEL;
 constexpr int32_t kTokenPages = IRIS_DECODE_TOKEN_PAGES;
 // IRIS_DECODE_TOKEN_PAGES, a fourth bit: the head-dim kernel's token-page
-// mode (decode_hd.hip; every page size at head_dim 64-224; the any-shape
+// mode (decode_hd.hip; every page size at head_dim 64-256; the any-shape
 // kernel's plan elsewhere).  The caller of a page size that is not 16 m
 // asks for it.
 // The selection bits of waves_per_block, or -1 if it is not a valid request
@@ -1460,10 +1460,17 @@ static bool mqa_preferred(int64_t batch, int64_t total_tokens, int64_t max_token
 // head (B=1, Hq=16, L=16384: 36.1 against 19.2, the sequence cut into 64
 // chunks for one merging workgroup), more units (B=64, L=1024: 34.9 against
 // 33.0) and ragged lengths (B=64, lengths in [16, 4096]: 47.5 against 42.5).
+// At head_dim 256 (where the general kernel holds one kv head a wave and
+// one wave a SIMD) it takes every call with two or more kv heads: 1.4-1.6x
+// the general kernel at every shape measured (B=8, L=8192: 47.9 against
+// 77.3 us; B=32, L=4096, 303 MB: 78.2 against 119.6; B=1, L=8192: 26.4
+// against 41.2; lengths in [128, 4096] at B=16: 41.0 against 59.2).
 constexpr int64_t kHdMinBytes = 4000000;
 static bool hd_preferred(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                          int64_t total_tokens, int64_t max_tokens) {
-    if ((head_dim != 64 && head_dim != 128) || num_kv_heads < 2) return false;
+    if (num_kv_heads < 2) return false;
+    if (head_dim == 256) return true;
+    if (head_dim != 64 && head_dim != 128) return false;
     const int64_t units = batch * num_kv_heads * query_blocks((int)(num_q_heads / num_kv_heads));
     const int64_t bytes = total_tokens * num_kv_heads * (head_dim + head_dim / 8);
     return units <= 256 && (head_dim == 128 || bytes >= kHdMinBytes) && bytes < kPagesMinBytes &&

@@ -13,7 +13,7 @@ namespace iris {
 IRIS_INTERNAL bool hd_supported(int64_t head_dim);
 
 // Token-page mode (any page size, tokens looked up one by one): head_dim
-// 64 to 224 in steps of 32, any number of kv heads.
+// 64 to 256 in steps of 32, any number of kv heads.
 IRIS_INTERNAL bool hd_tok_supported(int64_t head_dim, int64_t num_kv_heads);
 
 // Waves of the kernel's workgroups at head_dim (16 at 64, 12 at 96, 8 above).

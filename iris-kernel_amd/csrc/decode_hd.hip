@@ -6,7 +6,7 @@
 // (src/iris_kernel/fused_attention.py:11-220 in Hunter2030ZeRo/Iris-Kernel)
 // for head_dim 96, 160, 192 and 224 (G = 3, 5, 6, 7 scale groups of 32
 // dims), any number of kv heads and of query heads per kv head, pages of
-// 16 m tokens; in token-page mode (TOK) for head_dim 64 to 224 (G = 2-7)
+// 16 m tokens; in token-page mode (TOK) for head_dim 64 to 256 (G = 2-8)
 // and pages of any size, each token's page looked up through the block
 // table (ODD: the scale shifts per token, where G x Hkv is odd).  It computes the result of
 // `torch_eager_int4_paged_decode_attention`
@@ -336,6 +336,31 @@ struct Reads<7> {
                          IRIS_TR(6, 96) IRIS_S4(7, 8, 9, 10, 11, 12, 13, 14) IRIS_WAIT
                      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
                        IRIS_S4_OUT(s)
+                     : [tb] "v"(tb), [sb] "v"(sb)
+                     : "memory");
+    }
+};
+template <>
+struct Reads<8> {
+    static __device__ __forceinline__ void k(uint32_t kb0, uint32_t kb1, uint32_t sb, uint32_t (&k)[2][8],
+                                             u32x4_t (&s)[2][4]) {
+        asm volatile(IRIS_R32(0, kb0, 0) IRIS_R32(1, kb0, 16) IRIS_R32(2, kb0, 32) IRIS_R32(3, kb0, 48)
+                         IRIS_R32(4, kb0, 64) IRIS_R32(5, kb0, 80) IRIS_R32(6, kb0, 96) IRIS_R32(7, kb0, 112)
+                             IRIS_R32(8, kb1, 0) IRIS_R32(9, kb1, 16) IRIS_R32(10, kb1, 32) IRIS_R32(11, kb1, 48)
+                                 IRIS_R32(12, kb1, 64) IRIS_R32(13, kb1, 80) IRIS_R32(14, kb1, 96)
+                                     IRIS_R32(15, kb1, 112) IRIS_S4(16, 17, 18, 19, 20, 21, 22, 23) IRIS_WAIT
+                     : "=&v"(k[0][0]), "=&v"(k[0][1]), "=&v"(k[0][2]), "=&v"(k[0][3]), "=&v"(k[0][4]),
+                       "=&v"(k[0][5]), "=&v"(k[0][6]), "=&v"(k[0][7]), "=&v"(k[1][0]), "=&v"(k[1][1]),
+                       "=&v"(k[1][2]), "=&v"(k[1][3]), "=&v"(k[1][4]), "=&v"(k[1][5]), "=&v"(k[1][6]),
+                       "=&v"(k[1][7]), IRIS_S4_OUT(s)
+                     : [kb0] "v"(kb0), [kb1] "v"(kb1), [sb] "v"(sb)
+                     : "memory");
+    }
+    static __device__ __forceinline__ void v(uint32_t tb, uint32_t sb, int2v_t (&v)[8], u32x4_t (&s)[2][4]) {
+        asm volatile(IRIS_TR(0, 0) IRIS_TR(1, 16) IRIS_TR(2, 32) IRIS_TR(3, 48) IRIS_TR(4, 64) IRIS_TR(5, 80)
+                         IRIS_TR(6, 96) IRIS_TR(7, 112) IRIS_S4(8, 9, 10, 11, 12, 13, 14, 15) IRIS_WAIT
+                     : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+                       "=&v"(v[7]), IRIS_S4_OUT(s)
                      : [tb] "v"(tb), [sb] "v"(sb)
                      : "memory");
     }
@@ -921,7 +946,7 @@ bool hd_supported(int64_t head_dim) {
 }
 
 bool hd_tok_supported(int64_t head_dim, int64_t num_kv_heads) {
-    return head_dim % 32 == 0 && head_dim >= 64 && head_dim <= 224 && num_kv_heads > 0;
+    return head_dim % 32 == 0 && head_dim >= 64 && head_dim <= 256 && num_kv_heads > 0;
 }
 
 int hd_waves(int64_t head_dim) {
@@ -931,6 +956,7 @@ int hd_waves(int64_t head_dim) {
         case 128: return hd::Geo<4>::W;
         case 160: return hd::Geo<5>::W;
         case 192: return hd::Geo<6>::W;
+        case 256: return hd::Geo<8>::W;
         default: return hd::Geo<7>::W;
     }
 }
@@ -1091,6 +1117,7 @@ int hd_launch(const void* query, const void* k_data, const void* v_data, const v
             case 128: return launch_hd<4, true>(grid, s, a);
             case 160: return odd ? launch_hd<5, true, true>(grid, s, a) : launch_hd<5, true>(grid, s, a);
             case 192: return launch_hd<6, true>(grid, s, a);
+            case 256: return launch_hd<8, true>(grid, s, a);
             default: return odd ? launch_hd<7, true, true>(grid, s, a) : launch_hd<7, true>(grid, s, a);
         }
     }

@@ -53,7 +53,7 @@ DECODE_VALU_TILE = 0x200
 DECODE_ANY_KERNEL = 0x400
 # The token-page mode of the head-dim MFMA kernel (IRIS_DECODE_TOKEN_PAGES):
 # every page size, each token's page looked up through the block table, at
-# head_dim 64 to 224 (steps of 32); asked for at other head dims, the plan
+# head_dim 64 to 256 (steps of 32); asked for at other head dims, the plan
 # returns the any-shape kernel's.
 DECODE_TOKEN_PAGES = 0x800
 

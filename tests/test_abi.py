@@ -101,7 +101,8 @@ def test_decode_rejects_unsupported_shapes_before_launch():
     assert call(D=96, P=24, Hkv=1, nw=12 | tok, ct=12, mc=1) == 2  # 3 x 1 scale halves a row: odd
     assert call(D=96, P=3, NP=7, Hkv=1, nw=12 | tok, ct=12, mc=1) == 2  # ... in an odd pool: the any kernel
     assert call(D=96, P=3, NP=7, Hkv=1, nw=12 | tok, ct=3, mc=1) == 1   # (whose chunks are even tile counts)
-    assert call(D=256, P=8, nw=8 | tok, ct=8, mc=1) == 1    # head_dim 64 to 224
+    assert call(D=256, P=8, nw=8 | tok, ct=8, mc=1) == 2    # head_dim 64 to 256
+    assert call(D=288, P=8, nw=8 | tok, ct=8, mc=1) == 1
     assert call(D=96, P=24, nw=8 | tok, ct=12, mc=1) == 1   # its wave count only
     assert call(D=96, P=0, nw=12 | tok, ct=12, mc=1) == 1   # page_size >= 1
     assert call(D=96, P=200, nw=12 | tok, ct=12, mc=2) == 1  # chunks do not cover 4 x 200 tokens
@@ -336,7 +337,10 @@ def test_decode_plan_overrides_and_errors():
     assert decode_plan(2, 8, 1, 64, 64, waves_per_block=0x800)[2] == 16 | 0x800
     assert decode_plan(2, 8, 2, 96, 64, waves_per_block=0x800)[2] == 12 | 0x800
     assert decode_plan(2, 8, 1, 96, 64, waves_per_block=0x800)[2] == 12 | 0x800  # 3 halves a row
-    assert decode_plan(2, 8, 2, 256, 64, waves_per_block=0x800)[2] == 4 | 0x400
+    assert decode_plan(2, 8, 2, 256, 64, waves_per_block=0x800)[2] == 8 | 0x800
+    assert decode_plan(2, 8, 2, 256, 64)[2] == 8 | 0x800                        # the plan's own choice
+    assert decode_plan(2, 8, 1, 256, 64)[2] <= 4                                # one kv head: general
+    assert decode_plan(2, 8, 2, 256, 64, waves_per_block=4)[2] == 4
     assert decode_plan(2, 8, 2, 288, 64, waves_per_block=0x800)[2] == 4 | 0x400
     ct, mc, nw, ws = decode_plan(2, 8, 2, 160, 64, tokens_per_split=256, waves_per_block=0x800)
     assert (ct, mc, nw) == (8, 4, 8 | 0x800), (ct, mc, nw)
@@ -351,8 +355,9 @@ def test_decode_plan_overrides_and_errors():
     assert int4_decode_plan(2, 8, 2, 128, 1, 1000)[2] == 8 | 0x800
     assert int4_decode_plan(2, 8, 2, 128, 272, 10)[2] == 8 | 0x800
     assert int4_decode_plan(2, 8, 1, 96, 24, 10)[2] == 12 | 0x800
-    assert int4_decode_plan(2, 8, 1, 256, 24, 10)[2] == 4 | 0x400
-    assert int4_decode_plan(2, 8, 2, 256, 24, 10)[2] == 4 | 0x400
+    assert int4_decode_plan(2, 8, 1, 256, 24, 10)[2] == 8 | 0x800
+    assert int4_decode_plan(2, 8, 2, 256, 24, 10)[2] == 8 | 0x800
+    assert int4_decode_plan(2, 8, 2, 288, 24, 10)[2] == 4 | 0x400
     assert int4_decode_plan(2, 8, 2, 128, 24, 10, waves_per_block=0x400)[2] == 4 | 0x400
     assert int4_decode_plan(2, 8, 2, 128, 32, 10)[2] in (4, 16, 8 | 0x800)
     assert int4_decode_plan(2, 8, 2, 128, 48, 10)[2] in (1, 2, 3, 4, 16, 8 | 0x800)

@@ -1,7 +1,7 @@
 """INT4 decode on the any-shape kernel: head dims that are multiples of 32
 (32 to 512; 96, 160, 192 and 224 have an MFMA kernel of their own, and
-the token-page mode of that kernel takes most page sizes that are not 16 m
-by default, so the kernel is asked for here), page sizes that are not
+the token-page mode of that kernel takes every page size at head_dim 64 to
+256 by default, so the kernel is asked for here), page sizes that are not
 multiples of 16 (one token a page, 8, 24, 40), more than 16 query heads per kv head on such
 shapes -- everything the eager path takes (torch_eager_attention.py:72, :93
 of the reference) and its fused path refuses (fused_attention.py:390-403).
@@ -136,16 +136,16 @@ def test_any_kernel_forced_at_fast_shapes(device, cfg):
 
 def test_positional_handle_at_any_shape(device):
     # The sync-free positional handle plans for the widest batch the block
-    # table admits, at a 24-token page and head_dim 256 (the token-page mode
-    # takes head dims up to 224).
-    q, cache, bt, sl = _case(8, 2, 256, 24, [40, 900], 5)
-    assert int4_decode_plan(2, 8, 2, 256, 24, bt.shape[1])[2] & DECODE_ANY_KERNEL
+    # table admits, at a 24-token page and head_dim 288 (the token-page mode
+    # takes head dims up to 256).
+    q, cache, bt, sl = _case(8, 2, 288, 24, [40, 900], 5)
+    assert int4_decode_plan(2, 8, 2, 288, 24, bt.shape[1])[2] & DECODE_ANY_KERNEL
     want = torch_eager_int4_paged_decode_attention(q, *cache, bt, sl, page_size=24, out_dtype=torch.float32)
     gq, gbt, gsl = to(device, q, bt, sl)
     out = torch.empty(q.shape, dtype=torch.float32, device=device)
-    _int4_paged_decode_attention(gq, *to(device, *cache), gbt, gsl, out, 256, 24)
+    _int4_paged_decode_attention(gq, *to(device, *cache), gbt, gsl, out, 288, 24)
     torch.cuda.synchronize(device)
-    assert_attention_close(out, want, "positional handle D=256 P=24")
+    assert_attention_close(out, want, "positional handle D=288 P=24")
 
 
 def test_hip_graph_replay_at_any_shape(device):

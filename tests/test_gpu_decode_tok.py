@@ -3,7 +3,7 @@ head-dim MFMA kernel (csrc/decode_hd.hip, IRIS_DECODE_TOKEN_PAGES): each of
 a tile's 32 tokens finds its page through the block table, so the page size
 is free (the reference's eager path takes any page size,
 torch_eager_attention.py:72; its fused path only 16, fused_attention.py:
-390-403).  Head dims 64 to 224 in steps of 32, any number of kv heads (where
+390-403).  Head dims 64 to 256 in steps of 32, any number of kv heads (where
 head_dim / 32 x num_kv_heads is odd, a kv head's scales start on either
 half of a dword, by the token's slot, and the shift is taken per token).  Checked against the checker's eager attention
 (fp32 values within helpers.ATOL; fp16 outputs within one ulp), with one
@@ -74,6 +74,9 @@ def _check(device, q, cache, bt, sl, page, what, **kw):
     (6, 3, 128, 5, [1, 79, 81, 3000]),            # 3 kv heads at head_dim 128
     (16, 4, 128, 300, [1000, 4000]),              # 300-token pages
     (16, 2, 224, 16, [16, 32, 48, 900]),          # 16-token pages, asked for
+    (16, 2, 256, 8, [1, 300, 1000]),              # head_dim 256
+    (12, 3, 256, 24, [47, 1500]),                 # head_dim 256, 3 kv heads
+    (32, 8, 256, 16, [64, 2000]),                 # head_dim 256, 16-token pages (the plan's own choice)
 ])
 def test_token_pages_match_eager(device, hq, hkv, d, page, lens, tps):
     log(f"decode tok: Hq={hq} Hkv={hkv} D={d} P={page} lens={lens} split={tps}")
@@ -87,7 +90,7 @@ def test_token_pages_match_eager(device, hq, hkv, d, page, lens, tps):
     log(f"decode tok: max-abs err fp32 {e32:.2e} fp16 {e16:.2e} (plan {plan})")
 
 
-@pytest.mark.parametrize("d,page", [(64, 8), (96, 24), (128, 1), (160, 40), (192, 8), (224, 3)])
+@pytest.mark.parametrize("d,page", [(64, 8), (96, 24), (128, 1), (160, 40), (192, 8), (224, 3), (256, 12)])
 def test_token_pages_agree_with_the_any_kernel(device, d, page):
     # The two kernels that serve these page sizes, on one case with many
     # chunks: within the same bound of each other as of the eager result.

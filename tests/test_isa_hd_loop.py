@@ -1,6 +1,6 @@
 """The head_dim 96-224 decode kernel's tile loop, checked in its compiled
 gfx950 code (csrc/decode_hd.hip, every G instance of both modes: pages of
-16 m tokens, and token pages at head_dim 64-224, with the per-token scale
+16 m tokens, and token pages at head_dim 64-256, with the per-token scale
 shifts of odd scale rows at G = 3, 5, 7).
 
 A wave keeps the next tile's direct-to-LDS loads in flight while it
@@ -24,7 +24,7 @@ from iris_kernel import _build
 SRC = _build.CSRC / "decode_hd.hip"
 GROUPS = [3, 5, 6, 7]  # head_dim / 32
 # (G, token pages, per-token scale shifts)
-INSTANCES = ([(g, False, False) for g in GROUPS] + [(g, True, False) for g in (2, 3, 4, 5, 6, 7)]
+INSTANCES = ([(g, False, False) for g in GROUPS] + [(g, True, False) for g in (2, 3, 4, 5, 6, 7, 8)]
              + [(g, True, True) for g in (3, 5, 7)])
 
 
