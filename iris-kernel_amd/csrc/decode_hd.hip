@@ -401,6 +401,11 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     static_assert(TOK || !ODD, "per-token scale shifts are a token-page mode");
     using L = Geo<G>;
     constexpr int D = L::D, HB = L::HB, W = L::W, NK = L::NK, NS = L::NS, SP = L::SP, SLOT = L::SLOT;
+    // G = 8 in token-page mode: a kv head's 8 scales are one 16-byte-aligned
+    // 16 bytes, so one 16-byte load a token covers both scale tensors (K
+    // scales in lanes 0-31, V scales in lanes 32-63)
+    constexpr bool S16 = TOK && G == 8;
+    static_assert(!S16 || (SP == 4 && L::VS_OFF == L::KS_OFF + 512), "the 16-byte scale load's LDS layout");
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -578,6 +583,18 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
                 __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(a.v_data + off),
                                                  (IRIS_LDS void*)(dst + L::V_OFF + 1024 * i), 16, 0, 0);
             }
+        }
+        if constexpr (S16) {
+            // G = 8: a kv head's 8 scales are one 16-byte-aligned 16 bytes,
+            // so one load covers both tensors: lane t < 32 the K scales of
+            // token t (at KS_OFF + 16 t), lane 32 + t its V scales (at
+            // VS_OFF + 16 t = KS_OFF + 512 + 16 t)
+            const uint32_t st = __builtin_amdgcn_ds_bpermute(4 * (lane & 31), (int)slots);
+            const int64_t off = ((int64_t)st * srow_halves + kvh * G) * 2;
+            __builtin_amdgcn_global_load_lds(
+                reinterpret_cast<const void*>((lane < 32 ? a.k_scale : a.v_scale) + off),
+                (IRIS_LDS void*)(dst + L::KS_OFF), 16, 0, 0);
+            return;
         }
 #pragma unroll
         for (int i = 0; i < NS; ++i) {
@@ -778,7 +795,7 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     // tile ahead of the data: iteration s reads the entries of tile s + 1
     // (loaded at s - 1, before the data of tile s), issues the entries of
     // tile s + 2, then the data of tile s + 1.
-    constexpr int JOBS = 2 * NK + 2 * NS;
+    constexpr int JOBS = 2 * NK + (S16 ? 1 : 2 * NS);
     static_assert(JOBS + 2 < 64, "vmcnt range");
     const uint32_t ring_addr = lds_addr(ring);
     uint32_t odd_cur = 0, odd_next = 0;  // (ODD) the scale shifts of tiles s and s + 1

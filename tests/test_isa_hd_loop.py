@@ -28,12 +28,15 @@ INSTANCES = ([(g, False, False) for g in GROUPS] + [(g, True, False) for g in (2
              + [(g, True, True) for g in (3, 5, 7)])
 
 
-def jobs_of(g: int) -> int:
+def jobs_of(g: int, tok: bool) -> int:
     """Load instructions of one tile: 16-byte code loads (32 g pieces of 64
     lanes) and 4-byte scale loads (2 or 4 dwords a token: g halves from the
-    first, on the second half of a dword only where g is odd), for K and V."""
+    first, on the second half of a dword only where g is odd), for K and V;
+    at g = 8 in token-page mode one 16-byte load a token for both scale
+    tensors."""
     sp = 2 if (g + (g & 1)) // 2 <= 2 else 4
-    return 2 * ((32 * g + 63) // 64) + 2 * (32 * sp // 64)
+    scale_jobs = 1 if (tok and g == 8) else 2 * (32 * sp // 64)
+    return 2 * ((32 * g + 63) // 64) + scale_jobs
 
 
 @pytest.fixture(scope="module")
@@ -84,7 +87,7 @@ def test_tile_loop_is_the_tile_loop(asm, g, tok, odd):
 @pytest.mark.parametrize("g,tok,odd", INSTANCES)
 def test_tile_loop_waits_only_for_its_own_tiles(asm, g, tok, odd):
     loop = tile_loop(kernel(asm, g, tok, odd))
-    jobs = jobs_of(g)
+    jobs = jobs_of(g, tok)
     loads = sum(1 for l in loop if l.startswith("global_load_lds"))
     waits = {int(m) for l in loop if l.startswith("s_waitcnt") for m in re.findall(r"vmcnt\((\d+)\)", l)}
     # one tile in flight while one is computed (the last tile's vmcnt(0) may
