@@ -78,8 +78,9 @@ struct Geo {
     // scale dwords a token needs (at most): G halves from its first one, which
     // is the second half of a dword only where G is odd
     static constexpr int SD = (G_ + (G_ & 1)) / 2;
-    static constexpr int SP = SD <= 2 ? 2 : 4;               // scale dwords a token occupies in LDS
-    static constexpr int NS = 32 * SP / 64;                  // 4-byte loads a scale tensor a tile
+    static constexpr int SP = SD <= 1 ? 1 : SD <= 2 ? 2 : 4;  // scale dwords a token occupies in LDS
+    static constexpr int NS = (32 * SP + 63) / 64;           // 4-byte loads a scale tensor a tile
+    static constexpr int NSR = SP == 1 ? 1 : SP == 2 ? 2 : 4;  // 16-byte scale reads a half tile
     static constexpr int NA = (G_ + 1) / 2;                  // aligned scale dwords a token
     // Slot: [K pieces 32 G x 16 B (area KA)][V pieces (KA)][K scales 32 x SP dwords][V scales]
     static constexpr int K_OFF = 0, V_OFF = KA, KS_OFF = 2 * KA, VS_OFF = 2 * KA + 128 * SP;
@@ -221,18 +222,18 @@ __device__ __forceinline__ float load_sc1(const float* p) {
 template <int G>
 struct Reads;
 template <>
-struct Reads<2> {
+struct Reads<2> {  // one scale dword a token: tokens 16 e + 4 jq .. + 3 in one 16-byte read at sb + 64 e
     static __device__ __forceinline__ void k(uint32_t kb0, uint32_t kb1, uint32_t sb, uint32_t (&k)[2][2],
-                                             u32x4_t (&s)[2][2]) {
+                                             u32x4_t (&s)[2][1]) {
         asm volatile(IRIS_R32(0, kb0, 0) IRIS_R32(1, kb0, 16) IRIS_R32(2, kb1, 0) IRIS_R32(3, kb1, 16)
-                         IRIS_S2(4, 5, 6, 7) IRIS_WAIT
-                     : "=&v"(k[0][0]), "=&v"(k[0][1]), "=&v"(k[1][0]), "=&v"(k[1][1]), IRIS_S2_OUT(s)
+                         IRIS_R128(4, 0) IRIS_R128(5, 64) IRIS_WAIT
+                     : "=&v"(k[0][0]), "=&v"(k[0][1]), "=&v"(k[1][0]), "=&v"(k[1][1]), "=&v"(s[0][0]), "=&v"(s[1][0])
                      : [kb0] "v"(kb0), [kb1] "v"(kb1), [sb] "v"(sb)
                      : "memory");
     }
-    static __device__ __forceinline__ void v(uint32_t tb, uint32_t sb, int2v_t (&v)[2], u32x4_t (&s)[2][2]) {
-        asm volatile(IRIS_TR(0, 0) IRIS_TR(1, 16) IRIS_S2(2, 3, 4, 5) IRIS_WAIT
-                     : "=&v"(v[0]), "=&v"(v[1]), IRIS_S2_OUT(s)
+    static __device__ __forceinline__ void v(uint32_t tb, uint32_t sb, int2v_t (&v)[2], u32x4_t (&s)[2][1]) {
+        asm volatile(IRIS_TR(0, 0) IRIS_TR(1, 16) IRIS_R128(2, 0) IRIS_R128(3, 64) IRIS_WAIT
+                     : "=&v"(v[0]), "=&v"(v[1]), "=&v"(s[0][0]), "=&v"(s[1][0])
                      : [tb] "v"(tb), [sb] "v"(sb)
                      : "memory");
     }
@@ -379,14 +380,15 @@ struct Reads<8> {
 // bits): half c & 1 of dword c / 2 is group c.  Dwords past the loaded ones
 // reach only halves that are never used.
 template <int G>
-__device__ __forceinline__ void aligned_scales(const u32x4_t (&raw)[2][Geo<G>::SP == 2 ? 2 : 4], int e, int i,
+__device__ __forceinline__ void aligned_scales(const u32x4_t (&raw)[2][Geo<G>::NSR], int e, int i,
                                                uint32_t shift, uint32_t (&out)[Geo<G>::NA]) {
     constexpr int SP = Geo<G>::SP;
     uint32_t w[SP];
 #pragma unroll
     for (int j = 0; j < SP; ++j) {
         if constexpr (SP == 4) w[j] = raw[e][i][j];
-        else w[j] = raw[e][i >> 1][2 * (i & 1) + j];
+        else if constexpr (SP == 2) w[j] = raw[e][i >> 1][2 * (i & 1) + j];
+        else w[j] = raw[e][0][i];
     }
 #pragma unroll
     for (int c = 0; c < Geo<G>::NA; ++c) out[c] = __builtin_amdgcn_alignbit(c + 1 < SP ? w[c + 1] : 0u, w[c], shift);
@@ -406,6 +408,12 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     // scales in lanes 0-31, V scales in lanes 32-63)
     constexpr bool S16 = TOK && G == 8;
     static_assert(!S16 || (SP == 4 && L::VS_OFF == L::KS_OFF + 512), "the 16-byte scale load's LDS layout");
+    // G = 2 (one scale dword a kv head, token pages only): one 4-byte load a
+    // token covers both tensors the same way (K at KS_OFF + 4 t, V at
+    // VS_OFF + 4 t = KS_OFF + 128 + 4 t)
+    constexpr bool S4 = TOK && G == 2;
+    static_assert(TOK || SP > 1, "one-dword scale rows: token-page mode only");
+    static_assert(!S4 || (SP == 1 && L::VS_OFF == L::KS_OFF + 128), "the 4-byte scale load's LDS layout");
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -584,16 +592,15 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
                                                  (IRIS_LDS void*)(dst + L::V_OFF + 1024 * i), 16, 0, 0);
             }
         }
-        if constexpr (S16) {
-            // G = 8: a kv head's 8 scales are one 16-byte-aligned 16 bytes,
+        if constexpr (S16 || S4) {
+            // G = 8 or 2: a kv head's scales are one aligned 16 or 4 bytes,
             // so one load covers both tensors: lane t < 32 the K scales of
-            // token t (at KS_OFF + 16 t), lane 32 + t its V scales (at
-            // VS_OFF + 16 t = KS_OFF + 512 + 16 t)
+            // token t, lane 32 + t its V scales (right after the K area)
             const uint32_t st = __builtin_amdgcn_ds_bpermute(4 * (lane & 31), (int)slots);
             const int64_t off = ((int64_t)st * srow_halves + kvh * G) * 2;
-            __builtin_amdgcn_global_load_lds(
-                reinterpret_cast<const void*>((lane < 32 ? a.k_scale : a.v_scale) + off),
-                (IRIS_LDS void*)(dst + L::KS_OFF), 16, 0, 0);
+            const void* const src = reinterpret_cast<const void*>((lane < 32 ? a.k_scale : a.v_scale) + off);
+            if constexpr (S16) __builtin_amdgcn_global_load_lds(src, (IRIS_LDS void*)(dst + L::KS_OFF), 16, 0, 0);
+            else __builtin_amdgcn_global_load_lds(src, (IRIS_LDS void*)(dst + L::KS_OFF), 4, 0, 0);
             return;
         }
 #pragma unroll
@@ -652,7 +659,7 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     uint32_t shift[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) shift[i] = (uint32_t)((((i * a.n_kv_heads + kvh) * G) & 1) * 16);
-    constexpr int NSR = SP == 2 ? 2 : 4;  // 16-byte scale reads a half tile
+    constexpr int NSR = L::NSR;  // 16-byte scale reads a half tile
 
     const float c24 = a.log2_scale * 16777216.0f;  // MFMA units -> base-2 logits
     const float lazy = 2.0f / c24;                 // rescale when a maximum grows by more (base 2)
@@ -795,7 +802,7 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     // tile ahead of the data: iteration s reads the entries of tile s + 1
     // (loaded at s - 1, before the data of tile s), issues the entries of
     // tile s + 2, then the data of tile s + 1.
-    constexpr int JOBS = 2 * NK + (S16 ? 1 : 2 * NS);
+    constexpr int JOBS = 2 * NK + (S16 || S4 ? 1 : 2 * NS);
     static_assert(JOBS + 2 < 64, "vmcnt range");
     const uint32_t ring_addr = lds_addr(ring);
     uint32_t odd_cur = 0, odd_next = 0;  // (ODD) the scale shifts of tiles s and s + 1

@@ -32,10 +32,11 @@ def jobs_of(g: int, tok: bool) -> int:
     """Load instructions of one tile: 16-byte code loads (32 g pieces of 64
     lanes) and 4-byte scale loads (2 or 4 dwords a token: g halves from the
     first, on the second half of a dword only where g is odd), for K and V;
-    at g = 8 in token-page mode one 16-byte load a token for both scale
-    tensors."""
-    sp = 2 if (g + (g & 1)) // 2 <= 2 else 4
-    scale_jobs = 1 if (tok and g == 8) else 2 * (32 * sp // 64)
+    at g = 2 and 8 in token-page mode one 4- or 16-byte load a token for
+    both scale tensors."""
+    sd = (g + (g & 1)) // 2
+    sp = 1 if sd <= 1 else 2 if sd <= 2 else 4
+    scale_jobs = 1 if (tok and g in (2, 8)) else 2 * ((32 * sp + 63) // 64)
     return 2 * ((32 * g + 63) // 64) + scale_jobs
 
 
