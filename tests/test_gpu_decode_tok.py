@@ -204,3 +204,39 @@ def test_token_pages_at_the_benchmark_shape(device):
     out, _, _ = _check(device, q, cache, bt, sl, 16, "tok at B=1", waves_per_block=DECODE_TOKEN_PAGES)
     ref, _, _ = _check(device, q, cache, bt, sl, 16, "general at B=1", waves_per_block=4)
     assert_attention_close(out, ref, "tok against the general kernel")
+
+
+@pytest.mark.parametrize("hq,hkv,d,page", [
+    (8, 1, 96, 3),      # odd scale rows (per-token shifts), an odd pool: the any-shape kernel
+    (8, 1, 96, 4),      # odd scale rows, an even pool: the token-page mode
+    (16, 2, 256, 5),    # head_dim 256: 16-byte scale loads
+    (8, 2, 64, 7),      # head_dim 64: 4-byte scale loads
+    (8, 2, 128, 1),     # one token a page
+    (6, 3, 160, 9),     # odd scale rows, odd pool
+])
+def test_token_pages_read_the_pool_to_its_last_byte(device, hq, hkv, d, page):
+    # Every page of the pool in use and every sequence filling its table
+    # row, the pool's last page among them: the loads of the last slot's last
+    # kv head end at the tensors' last byte (checked against the eager
+    # attention, with and without split-KV).
+    lens = [25 * page, 40 * page - 1, 33 * page]
+    cols = 40
+    g = torch.Generator().manual_seed(d + page + hkv)
+    n_pages = len(lens) * cols
+    pool = []
+    for _ in range(2):
+        x = (torch.randn(n_pages, page, hkv, d, generator=g) * 1.5).to(torch.float16)
+        codes, scales = quantize_int4_groupwise(x, 32)
+        pool.append((pack_int4(codes), scales))
+    (kd, ks), (vd, vs) = pool
+    perm = torch.randperm(n_pages, generator=g)
+    perm = torch.cat([perm[perm != n_pages - 1], torch.tensor([n_pages - 1])])  # the last page last
+    bt = perm.view(len(lens), cols).flip(0).contiguous().to(torch.int32)   # ... in sequence 0's row
+    q = torch.randn(len(lens), hq, d, generator=g).to(torch.float16)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    sl[0] = cols * page  # the row's last token lies on the pool's last page
+    kw = {"waves_per_block": DECODE_TOKEN_PAGES} if page % 16 == 0 else {}
+    for tps in (0, 128):
+        _, e32, e16 = _check(device, q, (kd, vd, ks, vs), bt, sl, page,
+                             f"pool end Hkv={hkv} D={d} P={page} split={tps}", tokens_per_split=tps, **kw)
+        log(f"decode tok: pool end Hkv={hkv} D={d} P={page} split={tps}: fp32 {e32:.2e} fp16 {e16:.2e}")
