@@ -180,3 +180,27 @@ def test_hd_workspace_shared_with_other_kernels(device):
         torch.cuda.synchronize(device)
         assert_attention_close(out, wants[d][:n], f"D={d} batch {n} waves {waves}")
 
+
+
+@pytest.mark.parametrize("hq,hkv,d,page", [(8, 1, 96, 16), (6, 3, 160, 48), (8, 2, 224, 32), (5, 5, 192, 16)])
+def test_hd_reads_the_pool_to_its_last_byte(device, hq, hkv, d, page):
+    # Every page of the pool in use, the pool's last page at the end of a
+    # full table row: the last kv head's code and scale loads of the pool's
+    # last token end at the tensors' last byte.
+    cols = 24
+    g = torch.Generator().manual_seed(d + page + hkv)
+    n_pages = 3 * cols
+    pool = []
+    for _ in range(2):
+        x = (torch.randn(n_pages, page, hkv, d, generator=g) * 1.5).to(torch.float16)
+        codes, scales = quantize_int4_groupwise(x, 32)
+        pool.append((pack_int4(codes), scales))
+    (kd, ks), (vd, vs) = pool
+    perm = torch.randperm(n_pages, generator=g)
+    perm = torch.cat([perm[perm != n_pages - 1], torch.tensor([n_pages - 1])])
+    bt = perm.view(3, cols).flip(0).contiguous().to(torch.int32)  # the last page at the end of row 0
+    q = torch.randn(3, hq, d, generator=g).to(torch.float16)
+    sl = torch.tensor([cols * page, 17 * page - 3, 5 * page], dtype=torch.int32)
+    for tps in (0, 128):
+        _check(device, q, (kd, vd, ks, vs), bt, sl, page, f"pool end Hkv={hkv} D={d} P={page} split={tps}",
+               tokens_per_split=tps)
