@@ -114,8 +114,9 @@ struct Args {
     float* part_ml;      // [B][max_chunks][Hq][2] (m, l), base-2 logits
     int out_f32;
     int n_q_heads, n_kv_heads, group, q_blocks;
-    int n_units;    // batch x q_blocks x max_chunks
-    int seq_units;  // batch x q_blocks: the units of one chunk index
+    int n_units;         // batch x max_chunks
+    int seq_units;       // batch: the units of one chunk index
+    int n_heads_blocks;  // n_kv_heads x q_blocks: the workgroups of a unit
     int max_chunks, chunk_tiles;
     int max_pages;            // 16-token pages a block-table row addresses
     int bt_cols, page_code;   // block-table columns; the page code of virtual_page (page_size = 16 m)
@@ -420,29 +421,30 @@ __global__ __launch_bounds__(64 * Geo<G>::W) void int4_decode_hd_kernel(Args a) 
     const int n = lane & 15;   // MFMA row (A) or column (B, C): token or query head
     const int jq = lane >> 4;  // MFMA k-chunk (A, B) or row quad (C)
 
-    // ---- (kv head, unit = (chunk, sequence b, query block), chunk
+    // ---- ((kv head, query block), unit = (chunk, sequence b), chunk
     // slowest).  Workgroups are dispatched to the 8 XCDs in turn (workgroup
     // i to XCD i % 8), and a kv head's rows are only 16 G of each token's
-    // Hkv 16 G bytes: the kv heads of one unit run on one XCD, one after
-    // another (k = i / 8, unit (k / Hkv) 8 + i % 8, kv head k % Hkv), so the
-    // cache lines they share are fetched into one L2.  With the chunk index
-    // slowest, each XCD gets its share of every chunk index (chunks past a
-    // sequence's end, which return at once, would otherwise leave whole XCDs
-    // idle when the table is wider than the sequences); within chunk c the
-    // (sequence, query block) index is rotated by c, so a sequence's chunks
-    // run on different XCDs (a long sequence of a ragged batch would
+    // Hkv 16 G bytes, which every query block of the kv head reads: the
+    // (kv head, query block) pairs of one unit run on one XCD, one after
+    // another (k = i / 8, unit (k / (Hkv Q)) 8 + i % 8, pair k % (Hkv Q)),
+    // so the cache lines they share are fetched into one L2.  With the
+    // chunk index slowest, each XCD gets its share of every chunk index
+    // (chunks past a sequence's end, which return at once, would otherwise
+    // leave whole XCDs idle when the table is wider than the sequences);
+    // within chunk c the sequence index is rotated by c, so a sequence's
+    // chunks run on different XCDs (a long sequence of a ragged batch would
     // otherwise load one XCD's share of the bandwidth).  The grid is padded
     // to whole groups of 8 units; padding workgroups return at once.  The
     // divisions run on the VALU; readfirstlane keeps the results, and all
     // that derives from them (the loop bounds among it), scalar.
     const int k_x = blockIdx.x >> 3;
-    const int kvh = __builtin_amdgcn_readfirstlane(k_x % a.n_kv_heads);
-    const int unit = __builtin_amdgcn_readfirstlane((k_x / a.n_kv_heads) * 8 + (blockIdx.x & 7));
+    const int hb = __builtin_amdgcn_readfirstlane(k_x % a.n_heads_blocks);  // (kv head, query block)
+    const int kvh = __builtin_amdgcn_readfirstlane(hb / a.q_blocks);
+    const int qb = __builtin_amdgcn_readfirstlane(hb - kvh * a.q_blocks);
+    const int unit = __builtin_amdgcn_readfirstlane((k_x / a.n_heads_blocks) * 8 + (blockIdx.x & 7));
     if (unit >= a.n_units) return;
     const int chunk = __builtin_amdgcn_readfirstlane(unit / a.seq_units);
-    const int rest = __builtin_amdgcn_readfirstlane(rotate_back(unit - chunk * a.seq_units, chunk, a.seq_units));
-    const int qb = __builtin_amdgcn_readfirstlane(rest % a.q_blocks);
-    const int b = __builtin_amdgcn_readfirstlane(rest / a.q_blocks);
+    const int b = __builtin_amdgcn_readfirstlane(rotate_back(unit - chunk * a.seq_units, chunk, a.seq_units));
     const int t_begin = chunk * a.chunk_tiles;
     const int p0 = 2 * t_begin;  // first 16-token page of the chunk
     const int32_t* bt = a.block_table + (int64_t)b * a.bt_cols;
@@ -1093,8 +1095,8 @@ int hd_launch(const void* query, const void* k_data, const void* v_data, const v
     const int64_t g = num_q_heads / num_kv_heads;
     const int64_t q_blocks = (g + hd::kHeads - 1) / hd::kHeads;
     if (max_chunks > 1 && num_kv_heads * q_blocks > kCountersPerSeq) return kInvalidArgument;
-    const int64_t units = batch * q_blocks * (int64_t)max_chunks;
-    const int64_t nblocks = (units + 7) / 8 * 8 * num_kv_heads;  // whole groups of 8 units (XCD order)
+    const int64_t units = batch * (int64_t)max_chunks;
+    const int64_t nblocks = (units + 7) / 8 * 8 * num_kv_heads * q_blocks;  // whole groups of 8 units (XCD order)
     if (nblocks > 0x7FFFFFFF || num_q_heads > 0x7FFFFFFF) return kInvalidArgument;
     hd::Args a;
     a.q = (const half_t*)query;
@@ -1111,7 +1113,8 @@ int hd_launch(const void* query, const void* k_data, const void* v_data, const v
     a.group = (int)g;
     a.q_blocks = (int)q_blocks;
     a.n_units = (int)units;
-    a.seq_units = (int)(batch * q_blocks);
+    a.seq_units = (int)batch;
+    a.n_heads_blocks = (int)(num_kv_heads * q_blocks);
     a.max_chunks = max_chunks;
     a.chunk_tiles = chunk_tiles;
     a.max_pages = (int)max_pages;
