@@ -1373,21 +1373,22 @@ constexpr int64_t kPagesMinBytes = 100000000;  // K/V bytes above which the page
 // the GQA shapes of 7-70B models), over batches of similar lengths (its one
 // workgroup per CU balances ragged batches worse than the general kernel's
 // many small ones) that read at least kPagesMinBytes of K/V.
-// Shapes none of these kernels has -- head_dim other than 64, 128 or 256,
-// page sizes that are not multiples of 16 (or past 256) -- run on the any-shape kernel
-// (decode_any.hip), named by a third bit, IRIS_DECODE_ANY_KERNEL: the plan
-// sets it for such head dims by itself; for such page sizes (which the
-// plan is not told) the caller asks for it, and a launch with such a page
-// size and no bit is refused.  The bit may also be asked for at any shape.
+// head_dim 96, 160, 192 and 224 at pages of 16 m tokens plan the head-dim
+// kernel (decode_hd.hip) with no bit.  Page sizes that are not multiples
+// of 16 up to 256 (which the plan is not told) need a fourth bit, which
+// the caller asks for: IRIS_DECODE_TOKEN_PAGES, the head-dim kernel's
+// token-page mode (every page size at head_dim 64-256; the plan also
+// returns it by itself where it prefers that kernel, hd_preferred below);
+// a launch with such a page size and no bit is refused.  Head dims no
+// other kernel has (32, 288-512) run on the any-shape kernel
+// (decode_any.hip), named by a third bit, IRIS_DECODE_ANY_KERNEL, which
+// the plan sets for them by itself (and returns for token-page requests
+// at such head dims); it may also be asked for at any shape.
 constexpr int32_t kWaveMask = 0xFF;
 constexpr int32_t kPageKernel = IRIS_DECODE_PAGE_KERNEL;
 constexpr int32_t kValuTile = IRIS_DECODE_VALU_TILE;
 constexpr int32_t kAnyKernel = IRIS_DECODE_ANY_KERNEL;
 constexpr int32_t kTokenPages = IRIS_DECODE_TOKEN_PAGES;
-// IRIS_DECODE_TOKEN_PAGES, a fourth bit: the head-dim kernel's token-page
-// mode (decode_hd.hip; every page size at head_dim 64-256; the any-shape
-// kernel's plan elsewhere).  The caller of a page size that is not 16 m
-// asks for it.
 // The selection bits of waves_per_block, or -1 if it is not a valid request
 // (at most one bit).
 static int32_t selection_of(int32_t waves_per_block) {

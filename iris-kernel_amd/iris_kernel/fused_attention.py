@@ -49,7 +49,7 @@ DECODE_VALU_TILE = 0x200
 # multiple of 32 up to 512, every page size.  The plan picks it by itself for
 # head dims other than 64, 96, 128, 160, 192, 224 and 256 (96-224 have an
 # MFMA kernel of their own); page sizes that are not a multiple of 16 up to
-# 256 ask for it or for DECODE_TOKEN_PAGES.
+# 256 ask for DECODE_TOKEN_PAGES (or for it).
 DECODE_ANY_KERNEL = 0x400
 # The token-page mode of the head-dim MFMA kernel (IRIS_DECODE_TOKEN_PAGES):
 # every page size, each token's page looked up through the block table, at
