@@ -22,16 +22,17 @@ IRIS_INTERNAL int hd_waves(int64_t head_dim);
 // Chunk plan: chunk_tiles (a multiple of the waves, at most 32 tiles of 32
 // tokens a wave) and max_chunks, a chunk about one CU's share of the tiles of
 // the (sequence, kv head, block of 16 query heads) units; workspace bytes for
-// the split.  total_tokens / max_tokens may be -1 (unknown).  max_pages counts the 16-token pages a table row addresses
-// (rounded up in token-page mode).
+// the split.  total_tokens / max_tokens may be -1 (unknown).  max_pages
+// counts the 16-token pages a table row addresses (rounded up in token-page
+// mode).
 IRIS_INTERNAL int hd_plan(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
                           int64_t max_pages, int64_t total_tokens, int64_t max_tokens, int32_t tokens_per_split,
                           bool token_pages,
                           int32_t* out_chunk_tiles, int32_t* out_max_chunks, int32_t* out_waves,
                           int64_t* out_workspace_bytes);
 
-// Launch: num_kv_heads x (batch x ceil(g / 16) x max_chunks, rounded up to 8)
-// workgroups (the kv heads of one unit on one XCD) of
+// Launch: num_kv_heads x ceil(g / 16) x (batch x max_chunks, rounded up to
+// 8) workgroups (the kv heads and query blocks of one unit on one XCD) of
 // `waves` (= hd_waves) waves; max_pages counts 16-token pages, page_code is
 // virtual_page's (common.h).  token_pages: pages of page_size tokens (any
 // size), the grid covering bt_cols x page_size tokens; page_code unused.
