@@ -19,9 +19,11 @@ paged decode attention over the 4096 tokens.
   pass where a GPU sleep lets the host queue every step first, so the events
   bracket kernel execution only (``append_us``).
 * Decode kernel time: one event pair around K back-to-back decode launches
-  on the launch stream (rotating over the replicas), i.e. the average launch
-  duration of the single decode kernel (split-KV combine fused in).
-  ``value`` = algorithmic decode bytes / that duration.
+  on the launch stream (rotating over the replicas, after 5 untimed ones),
+  i.e. the average launch duration of the single decode kernel (split-KV
+  combine fused in); the median of 3 such passes (all in
+  ``decode_us_passes``).  ``value`` = algorithmic decode bytes / that
+  duration.
 * ``roofline.traffic``: HBM bytes per decode launch measured with rocprofv3
   counters (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), read from
   profiles/decode_cfg2_traffic.json.
@@ -259,15 +261,27 @@ def main() -> int:
     # the cache replicas: the average launch duration of the decode kernel
     # (what rocprofv3 --kernel-trace reports per dispatch), without the
     # per-event overhead of the pass above.
-    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    torch.cuda._sleep(int(1e6) * n)
-    k0.record()
-    for i in range(n):
-        do_decode(i % reps)
-    k1.record()
-    torch.cuda.synchronize()
-    dec_mean = k0.elapsed_time(k1) * 1e3 / n
+    def back_to_back(fn, n_reps):
+        """Median over 3 passes of the mean launch duration (us) of n
+        back-to-back calls of fn: each pass queues a GPU sleep (so the host
+        enqueues every launch before the first runs), 5 untimed calls (the
+        clocks back at load after the sleep), then the timed n."""
+        k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        passes = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            torch.cuda._sleep(int(1e6) * n)
+            for i in range(5):
+                fn(i % n_reps)
+            k0.record()
+            for i in range(n):
+                fn(i % n_reps)
+            k1.record()
+            torch.cuda.synchronize()
+            passes.append(k0.elapsed_time(k1) * 1e3 / n)
+        return statistics.median(passes), passes
+
+    dec_mean, dec_passes = back_to_back(do_decode, reps)
     dbytes = decode_bytes(B, Hq, Hkv, D, lens)
     abytes = append_bytes(B, Hkv, D, len(set(new_pos.tolist())))
     achieved = dbytes / (dec_mean * 1e-6) / 1e9
@@ -297,6 +311,7 @@ def main() -> int:
         },
         "storage": "int4 codes + fp16 group-32 scales; fp16 MFMA operands, fp32 accumulate",
         "decode_us": round(dec_mean, 3),
+        "decode_us_passes": [round(x, 3) for x in dec_passes],
         "decode_us_per_op_event_p50": round(statistics.median(dec_op_us), 3),
         "decode_tokens_per_s": round(B / (dec_mean * 1e-6), 1),
         "decode_hbm_gbs": round(achieved, 1),
@@ -387,14 +402,7 @@ def main() -> int:
 
         for i in range(args.warmup):
             do_fp16(i % reps16)
-        torch.cuda.synchronize()
-        torch.cuda._sleep(int(1e6) * n)
-        k0.record()
-        for i in range(n):
-            do_fp16(i % reps16)
-        k1.record()
-        torch.cuda.synchronize()
-        f16_us = k0.elapsed_time(k1) * 1e3 / n
+        f16_us, f16_passes = back_to_back(do_fp16, reps16)
         f16_bytes = sum(lens) * Hkv * 4 * D + 2 * B * Hq * D * 2 + 4 * sum((x + 15) // 16 for x in lens) + 4 * B
         result["fp16_decode"] = {
             "workload": "same decode over an fp16 cache [NP, 16, Hkv, D] (the reference's matched FP16 baseline)",
@@ -402,6 +410,7 @@ def main() -> int:
             "hbm_gbs": round(f16_bytes / (f16_us * 1e-6) / 1e9, 1),
             "hbm_frac": round(f16_bytes / (f16_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "int4_speedup": round(f16_us / dec_mean, 3), "cache_replicas": reps16,
+            "us_passes": [round(x, 3) for x in f16_passes],
         }
         log(f"fp16 decode: {f16_us:.2f} us ({f16_bytes / (f16_us * 1e-6) / 1e9:.0f} GB/s); INT4 is "
             f"{f16_us / dec_mean:.2f}x faster")
