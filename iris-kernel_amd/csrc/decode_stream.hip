@@ -89,6 +89,11 @@ constexpr int kJobs = 3;            // loads per wave per slot
 constexpr int kMaxChunkTiles = 64;  // a chunk's 128 page ids fill two VGPRs
 constexpr int kMaxChunks = 64;      // partials the merge reads
 constexpr int kMergeBatch = 8;      // partials in flight per thread in the merge
+// Balanced mode: a long sequence's pieces (up to 18 at configuration 3) in
+// two round trips of 12 instead of three of 8; the merge after the last
+// arrival is on the critical path there (53.7-54.0 against 56.8-57.4 us).
+// 16 spilled 43 VGPRs (67.7 us).
+constexpr int kMergeBatchSeg = 12;
 // Chunks merged by the last of each group (two levels past 32): one merge
 // reads a partial in about 0.1 us past its ~1.2 us latency, a second level
 // costs a publish, an arrival and another merge's latency, so one level is
@@ -1009,7 +1014,7 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
             // Merge M partials (o / l at po, (m, l) at pm; partial `own` from LDS)
             // into the output, or into the group partial at (wo, wm): each thread
             // float4s of it, o = sum_c w_c (o / l)_c / sum_c w_c with
-            // w_c = l_c 2^(m_c - m*), kMergeBatch partials and their (m, l) in
+            // w_c = l_c 2^(m_c - m*), MB partials and their (m, l) in
             // flight, m* the running maximum.
             auto merge = [&](const float* po, const float* pm, int M, int own, bool to_out, float* wo,
                              float* wm) __attribute__((always_inline)) {
@@ -1021,11 +1026,12 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
                     const int h = 4 * e4 / D;
                     float mstar = -INFINITY, lsum = 0.0f;
                     float4_t acc = {0, 0, 0, 0};
-                    for (int c0 = 0; c0 < M; c0 += kMergeBatch) {
-                        float4_t oc[kMergeBatch];
-                        float2v_t ml[kMergeBatch];
+                    constexpr int MB = SEG ? kMergeBatchSeg : kMergeBatch;
+                    for (int c0 = 0; c0 < M; c0 += MB) {
+                        float4_t oc[MB];
+                        float2v_t ml[MB];
         #pragma unroll
-                        for (int cb = 0; cb < kMergeBatch; ++cb) {
+                        for (int cb = 0; cb < MB; ++cb) {
                             const int c = min(c0 + cb, M - 1);
                             if (c != own) {
                                 oc[cb] = load4_sc1(ro, (uint32_t)c * part_o + (uint32_t)e4 * 16);
@@ -1039,12 +1045,12 @@ __global__ __launch_bounds__(64 * kWaves) void int4_decode_stream_kernel(
                         // past M: a repeat of partial M - 1 with weight 0
                         float mb = mstar;
         #pragma unroll
-                        for (int cb = 0; cb < kMergeBatch; ++cb) mb = fmaxf(mb, ml[cb][0]);
+                        for (int cb = 0; cb < MB; ++cb) mb = fmaxf(mb, ml[cb][0]);
                         const float r = __builtin_amdgcn_exp2f(mstar - mb);  // 0 on the first batch
                         acc *= r;
                         lsum *= r;
         #pragma unroll
-                        for (int cb = 0; cb < kMergeBatch; ++cb) {
+                        for (int cb = 0; cb < MB; ++cb) {
                             const float w = c0 + cb < M ? ml[cb][1] * __builtin_amdgcn_exp2f(ml[cb][0] - mb) : 0.0f;
                             acc += oc[cb] * w;
                             lsum += w;
